@@ -1,0 +1,97 @@
+"""ctypes binding of libcdx.so, the gfx950 kernel library declared in include/cdx.h.
+
+This is the only place the package touches native code.  There is no CPU or
+PyTorch fallback: if the library is missing, or a tensor is not a bf16 tensor on a
+ROCm device, the call raises.  Every launch goes onto the caller's current torch
+stream and nothing synchronises the host.
+"""
+
+from __future__ import annotations
+
+import ctypes
+from pathlib import Path
+from typing import Optional
+
+import torch
+
+LIB_PATH = Path(__file__).resolve().parent / "libcdx.so"
+
+_lib = None
+
+_vp = ctypes.c_void_p
+_i64 = ctypes.c_int64
+_i32 = ctypes.c_int32
+
+# name -> (restype, argtypes), mirroring include/cdx.h
+_SIGNATURES = {
+    "cdx_version": (ctypes.c_int, []),
+    "cdx_last_error": (ctypes.c_char_p, []),
+    "cdx_add_rmsnorm_fwd": (ctypes.c_int, [_vp, _vp, _vp, ctypes.c_float, _i64, _i32, _vp, _vp, _vp]),
+    "cdx_route_workspace_bytes": (ctypes.c_size_t, [_i64, _i32]),
+    "cdx_route_plan": (ctypes.c_int, [_vp, _i64, _vp, _i64, _i32, _vp, _vp, _vp, _vp, _vp, _vp,
+                                      ctypes.c_size_t, _vp]),
+    "cdx_permute_rows": (ctypes.c_int, [_vp, _vp, _i64, _i64, _vp, _vp]),
+    "cdx_unpermute_rows": (ctypes.c_int, [_vp, _vp, _i64, _i64, _vp, _vp]),
+    "cdx_moe_swiglu_fwd": (ctypes.c_int, [_vp, _i64, _i32, _i32, _i32, _i32, _vp, _vp, _vp, _vp, _vp,
+                                          _vp, _vp]),
+    "cdx_grouped_gemm_fwd": (ctypes.c_int, [_vp, _i64, _i32, _i32, _i32, _vp, _vp, _vp, _vp]),
+    "cdx_mu_qkv_fwd": (ctypes.c_int, [_vp, _i64, _vp, _i64, _vp, _i64, _i64, _i32, _i32, _vp, _i64,
+                                      _vp]),
+}
+
+
+class NativeLibraryMissing(RuntimeError):
+    pass
+
+
+def lib():
+    """Load libcdx.so once (raises NativeLibraryMissing if it has not been built)."""
+    global _lib
+    if _lib is None:
+        if not LIB_PATH.exists():
+            raise NativeLibraryMissing(
+                f"{LIB_PATH} is missing: build it with `python complexity-deep_amd/build_native.py` "
+                "(or __graft_entry__.build()); there is no fallback path")
+        handle = ctypes.CDLL(str(LIB_PATH))
+        for name, (res, args) in _SIGNATURES.items():
+            fn = getattr(handle, name)
+            fn.restype = res
+            fn.argtypes = args
+        _lib = handle
+    return _lib
+
+
+def exported_symbols():
+    return list(_SIGNATURES)
+
+
+def check(rc: int, what: str) -> None:
+    if rc != 0:
+        msg = lib().cdx_last_error().decode(errors="replace")
+        raise RuntimeError(f"{what} failed (status {rc}): {msg}")
+
+
+def stream_of(t: torch.Tensor) -> int:
+    return torch.cuda.current_stream(t.device).cuda_stream
+
+
+def ptr(t: Optional[torch.Tensor]) -> Optional[int]:
+    return None if t is None else t.data_ptr()
+
+
+def require_device(*tensors: Optional[torch.Tensor], dtype: Optional[torch.dtype] = torch.bfloat16,
+                   what: str = "op") -> None:
+    """All tensors on one ROCm device (and of `dtype` if given)."""
+    dev = None
+    for t in tensors:
+        if t is None:
+            continue
+        if not t.is_cuda:
+            raise RuntimeError(f"{what}: tensors must be on a ROCm GPU (got {t.device}); "
+                               "the MI355X kernels have no CPU path")
+        if dtype is not None and t.dtype != dtype:
+            raise RuntimeError(f"{what}: expected {dtype}, got {t.dtype}")
+        if dev is None:
+            dev = t.device
+        elif t.device != dev:
+            raise RuntimeError(f"{what}: tensors on different devices ({dev} vs {t.device})")

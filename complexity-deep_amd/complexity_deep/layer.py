@@ -1,0 +1,104 @@
+"""Decoder block and mu guidance; interfaces of core/layer.py:28-190.
+
+``TransformerBlock.forward`` keeps the reference signature and returns
+(hidden_states, new_kv, mu).  Inside, the residual add before the MLP's norm is the
+fused add+RMSNorm kernel.  ``ComplexityModel`` drives the blocks through
+``forward_fused``, which also fuses the add after the MLP with the *next* norm (the
+next layer's input norm or the final norm) and reuses one routing plan for all
+layers.
+"""
+
+from __future__ import annotations
+
+from typing import Optional, Tuple
+
+import torch
+import torch.nn as nn
+import torch.nn.functional as F
+
+from .attention import ComplexityAttention
+from .mlp import SwiGLU
+from .normalization import RMSNorm, add_rms_norm
+from .token_routed_mlp import RoutePlan, TokenRoutedMLP
+
+
+class MuGuidance(nn.Module):
+    """mu = clamp(mu_param, mu_min, mu_max) + mu_proj(h); core/layer.py:28-61."""
+
+    def __init__(self, hidden_size: int, mu_min: float = 0.0, mu_max: float = 2.0):
+        super().__init__()
+        self.mu_min = mu_min
+        self.mu_max = mu_max
+        self.mu = nn.Parameter(torch.full((hidden_size,), (mu_min + mu_max) / 2))
+        self.mu_proj = nn.Linear(hidden_size, hidden_size, bias=False)
+        nn.init.zeros_(self.mu_proj.weight)
+
+    def forward(self, hidden_states: torch.Tensor) -> torch.Tensor:
+        return torch.clamp(self.mu, self.mu_min, self.mu_max) + F.linear(hidden_states, self.mu_proj.weight)
+
+
+class TransformerBlock(nn.Module):
+    """Pre-norm block: attention -> MLP -> mu guidance; core/layer.py:63-190."""
+
+    def __init__(self, hidden_size: int, intermediate_size: int, num_attention_heads: int,
+                 num_key_value_heads: int, max_position_embeddings: int = 2048,
+                 rms_norm_eps: float = 1e-6, rope_theta: float = 10000.0,
+                 attention_dropout: float = 0.0, use_token_routed_mlp: bool = True,
+                 num_experts: int = 4, vocab_size: int = 100_000, shared_expert: bool = True,
+                 token_frequencies: Optional[torch.Tensor] = None, use_qk_norm: bool = True,
+                 use_mu_guidance: bool = True):
+        super().__init__()
+        self.hidden_size = hidden_size
+        self.use_token_routed_mlp = use_token_routed_mlp
+        self.input_layernorm = RMSNorm(hidden_size, eps=rms_norm_eps)
+        self.self_attn = ComplexityAttention(
+            hidden_size=hidden_size, num_attention_heads=num_attention_heads,
+            num_key_value_heads=num_key_value_heads, max_position_embeddings=max_position_embeddings,
+            rope_theta=rope_theta, attention_dropout=attention_dropout, use_qk_norm=use_qk_norm)
+        self.post_attention_layernorm = RMSNorm(hidden_size, eps=rms_norm_eps)
+        if use_token_routed_mlp:
+            self.mlp = TokenRoutedMLP(hidden_size=hidden_size, intermediate_size=intermediate_size,
+                                      num_experts=num_experts, vocab_size=vocab_size,
+                                      shared_expert=shared_expert, token_frequencies=token_frequencies)
+        else:
+            self.mlp = SwiGLU(hidden_size=hidden_size, intermediate_size=intermediate_size)
+        self.use_mu_guidance = use_mu_guidance
+        self.mu_guidance = MuGuidance(hidden_size=hidden_size) if use_mu_guidance else None
+
+    def _mlp(self, x: torch.Tensor, token_ids, route: Optional[RoutePlan]) -> torch.Tensor:
+        if self.use_token_routed_mlp:
+            return self.mlp(x, token_ids=token_ids, route=route)
+        return self.mlp(x)
+
+    def forward(self, hidden_states: torch.Tensor, attention_mask: Optional[torch.Tensor] = None,
+                past_key_value: Optional[Tuple[torch.Tensor, torch.Tensor]] = None,
+                use_cache: bool = False, token_ids: Optional[torch.Tensor] = None,
+                mu_prev: Optional[torch.Tensor] = None):
+        normed = self.input_layernorm(hidden_states)
+        attn_out, new_kv = self.self_attn(normed, attention_mask=attention_mask,
+                                          past_key_value=past_key_value, use_cache=use_cache,
+                                          mu_prev=mu_prev)
+        ln = self.post_attention_layernorm
+        normed, h = add_rms_norm(attn_out, hidden_states, ln.weight, ln.eps)
+        h = h + self._mlp(normed, token_ids, None)
+        mu = self.mu_guidance(h) if self.mu_guidance is not None else None
+        return h, new_kv, mu
+
+    def forward_fused(self, h: torch.Tensor, normed: torch.Tensor, next_norm: RMSNorm,
+                      attention_mask=None, past_key_value=None, use_cache: bool = False,
+                      token_ids=None, mu_prev=None, route: Optional[RoutePlan] = None,
+                      want_mu: bool = True):
+        """One block given h (updated in place) and normed = input_layernorm(h).
+
+        Returns (h, next_norm(h_out), new_kv, mu) where the residual add after the MLP
+        is fused with ``next_norm``.  ``want_mu=False`` skips mu for the last layer,
+        whose mu the reference computes and then discards (modeling.py:199-200)."""
+        attn_out, new_kv = self.self_attn(normed, attention_mask=attention_mask,
+                                          past_key_value=past_key_value, use_cache=use_cache,
+                                          mu_prev=mu_prev)
+        ln = self.post_attention_layernorm
+        normed, _ = add_rms_norm(attn_out, h, ln.weight, ln.eps, residual_out=h)
+        mlp_out = self._mlp(normed, token_ids, route)
+        normed, _ = add_rms_norm(mlp_out, h, next_norm.weight, next_norm.eps, residual_out=h)
+        mu = self.mu_guidance(h) if (want_mu and self.mu_guidance is not None) else None
+        return h, normed, new_kv, mu

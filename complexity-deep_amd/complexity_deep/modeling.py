@@ -1,0 +1,331 @@
+"""Model, configuration and helpers; interfaces of models/config.py, models/modeling.py
+and models/utils.py.
+
+``ComplexityConfig`` is field-for-field the reference dataclass (config.py:13-109);
+``ComplexityModel`` registers the same modules in the same order, so that
+``torch.manual_seed(s); ComplexityModel(cfg)`` draws identical weights and the
+state_dict keys and shapes match (modeling.py:69-149).
+
+The forward (modeling.py:155-219) runs the hot path on the gfx950 kernels:
+  * one routing plan per distinct expert map, computed once per forward and shared
+    by every layer using that map (the reference re-routes in each layer);
+  * a plain RMSNorm for layer 0's input, then every residual add fused with the
+    norm that follows it (2L fused add+RMSNorm calls, the last one being the final
+    norm);
+  * the last layer's mu, which the reference computes and discards, is skipped.
+Embedding, attention core, o_proj, mu_proj and lm_head run as PyTorch-ROCm ops.
+"""
+
+from __future__ import annotations
+
+import inspect
+import json
+from dataclasses import dataclass
+from pathlib import Path
+from typing import Any, Dict, List, Optional, Tuple
+
+import torch
+import torch.nn as nn
+import torch.nn.functional as F
+
+from ._grad import forward_only
+from .layer import TransformerBlock
+from .normalization import RMSNorm, rms_norm
+from .token_routed_mlp import RoutePlan, route_plan
+
+
+@dataclass
+class ComplexityConfig:
+    vocab_size: int = 100_000
+    hidden_size: int = 768
+    intermediate_size: int = 2048
+    num_hidden_layers: int = 12
+    num_attention_heads: int = 12
+    num_key_value_heads: int = 4
+    max_position_embeddings: int = 2048
+    rope_theta: float = 10000.0
+    rms_norm_eps: float = 1e-6
+    attention_dropout: float = 0.0
+    hidden_act: str = "silu"
+    tie_word_embeddings: bool = True
+    initializer_range: float = 0.02
+    pad_token_id: int = 1
+    bos_token_id: int = 2
+    eos_token_id: int = 0
+    use_token_routed_mlp: bool = True
+    num_experts: int = 4
+    shared_expert: bool = True
+    use_mu_guidance: bool = True
+    use_qk_norm: bool = True
+
+    @classmethod
+    def complexity_tiny(cls) -> "ComplexityConfig":
+        return cls(hidden_size=256, intermediate_size=704, num_hidden_layers=6,
+                   num_attention_heads=4, num_key_value_heads=2)
+
+    @classmethod
+    def complexity_20m(cls) -> "ComplexityConfig":
+        return cls(hidden_size=320, intermediate_size=896, num_hidden_layers=8,
+                   num_attention_heads=8, num_key_value_heads=4)
+
+    @classmethod
+    def complexity_small(cls) -> "ComplexityConfig":
+        return cls(hidden_size=512, intermediate_size=1408, num_hidden_layers=8,
+                   num_attention_heads=8, num_key_value_heads=4)
+
+    @classmethod
+    def complexity_150m(cls) -> "ComplexityConfig":
+        return cls(hidden_size=768, intermediate_size=2048, num_hidden_layers=12,
+                   num_attention_heads=12, num_key_value_heads=4)
+
+    @classmethod
+    def complexity_350m(cls) -> "ComplexityConfig":
+        return cls(hidden_size=1280, intermediate_size=3456, num_hidden_layers=20,
+                   num_attention_heads=16, num_key_value_heads=4)
+
+    @classmethod
+    def complexity_1b(cls) -> "ComplexityConfig":
+        return cls(hidden_size=2048, intermediate_size=5632, num_hidden_layers=24,
+                   num_attention_heads=16, num_key_value_heads=8, num_experts=8)
+
+    def to_dict(self) -> dict:
+        return {k: v for k, v in self.__dict__.items() if not k.startswith("_")}
+
+    @classmethod
+    def from_dict(cls, d: dict) -> "ComplexityConfig":
+        known = set(inspect.signature(cls).parameters)
+        return cls(**{k: v for k, v in d.items() if k in known})
+
+
+@dataclass
+class ModelOutput:
+    logits: Optional[torch.Tensor] = None
+    last_hidden_state: Optional[torch.Tensor] = None
+    past_key_values: Optional[List[Tuple[torch.Tensor, torch.Tensor]]] = None
+
+
+@dataclass
+class CausalLMOutput:
+    loss: Optional[torch.Tensor] = None
+    logits: Optional[torch.Tensor] = None
+    past_key_values: Optional[List[Tuple[torch.Tensor, torch.Tensor]]] = None
+
+
+class ComplexityModel(nn.Module):
+    """Decoder-only Complexity transformer (embed -> L blocks -> norm -> tied lm_head)."""
+
+    def __init__(self, config: ComplexityConfig):
+        super().__init__()
+        self.config = config
+        self.embed_tokens = nn.Embedding(config.vocab_size, config.hidden_size)
+        self.layers = nn.ModuleList([
+            TransformerBlock(
+                hidden_size=config.hidden_size, intermediate_size=config.intermediate_size,
+                num_attention_heads=config.num_attention_heads,
+                num_key_value_heads=config.num_key_value_heads,
+                max_position_embeddings=config.max_position_embeddings,
+                rms_norm_eps=config.rms_norm_eps, rope_theta=config.rope_theta,
+                attention_dropout=config.attention_dropout,
+                use_token_routed_mlp=config.use_token_routed_mlp, num_experts=config.num_experts,
+                vocab_size=config.vocab_size, shared_expert=config.shared_expert,
+                use_qk_norm=config.use_qk_norm, use_mu_guidance=config.use_mu_guidance)
+            for _ in range(config.num_hidden_layers)
+        ])
+        self.norm = RMSNorm(config.hidden_size, eps=config.rms_norm_eps)
+        self.lm_head = nn.Linear(config.hidden_size, config.vocab_size, bias=False)
+        if config.tie_word_embeddings:
+            self.lm_head.weight = self.embed_tokens.weight
+        if config.use_mu_guidance:
+            self.mu_init = nn.Parameter(torch.zeros(1, 1, config.hidden_size))
+        self.apply(self._init_weights)
+        self._init_residual_scaling()
+        self._map_groups: List[int] = []
+        self._map_key = None
+
+    # ---- initialisation (modeling.py:117-149) --------------------------------
+    def _init_weights(self, module: nn.Module) -> None:
+        std = self.config.initializer_range
+        if isinstance(module, nn.Linear):
+            nn.init.normal_(module.weight, mean=0.0, std=std)
+            if module.bias is not None:
+                nn.init.zeros_(module.bias)
+        elif isinstance(module, nn.Embedding):
+            nn.init.normal_(module.weight, mean=0.0, std=std)
+
+    def _init_residual_scaling(self) -> None:
+        std = self.config.initializer_range / (2 * self.config.num_hidden_layers) ** 0.5
+        for layer in self.layers:
+            nn.init.normal_(layer.self_attn.o_proj.weight, mean=0.0, std=std)
+            mlp = layer.mlp
+            if isinstance(getattr(mlp, "down_proj_w", None), nn.Parameter):
+                nn.init.normal_(mlp.down_proj_w, mean=0.0, std=std)
+            elif isinstance(getattr(mlp, "down_proj", None), nn.Linear):
+                nn.init.normal_(mlp.down_proj.weight, mean=0.0, std=std)
+            if isinstance(getattr(mlp, "shared_down", None), nn.Linear):
+                nn.init.normal_(mlp.shared_down.weight, mean=0.0, std=std)
+
+    # ---- routing plans ---------------------------------------------------------
+    def _map_grouping(self) -> List[int]:
+        """Index of the first layer whose expert map equals each layer's map.
+
+        Re-evaluated only when a map buffer is replaced or modified (it compares
+        maps on the device, which synchronises once at that point)."""
+        maps = [layer.mlp.token_to_expert if layer.use_token_routed_mlp else None for layer in self.layers]
+        key = tuple(None if m is None else (m.data_ptr(), m._version, m.device) for m in maps)
+        if key != self._map_key:
+            canon: List[int] = []
+            for i, m in enumerate(maps):
+                owner = i
+                if m is not None:
+                    for j in range(i):
+                        if canon[j] == j and maps[j] is not None and maps[j].shape == m.shape \
+                                and torch.equal(maps[j], m):
+                            owner = j
+                            break
+                canon.append(owner)
+            self._map_groups = canon
+            self._map_key = key
+        return self._map_groups
+
+    def route_plans(self, input_ids: torch.Tensor) -> List[Optional[RoutePlan]]:
+        groups = self._map_grouping()
+        plans: Dict[int, RoutePlan] = {}
+        out: List[Optional[RoutePlan]] = []
+        for i, layer in enumerate(self.layers):
+            if not layer.use_token_routed_mlp:
+                out.append(None)
+                continue
+            g = groups[i]
+            if g not in plans:
+                plans[g] = route_plan(input_ids, layer.mlp.token_to_expert, layer.mlp.num_experts)
+            out.append(plans[g])
+        return out
+
+    # ---- forward (modeling.py:155-219) --------------------------------------------
+    def forward(self, input_ids: torch.Tensor, attention_mask: Optional[torch.Tensor] = None,
+                labels: Optional[torch.Tensor] = None,
+                past_key_values: Optional[List[Tuple[torch.Tensor, torch.Tensor]]] = None,
+                use_cache: bool = False) -> CausalLMOutput:
+        forward_only("ComplexityModel", *self.parameters())
+        B, S = input_ids.shape
+        h = self.embed_tokens(input_ids)
+        mu_prev = self.mu_init.expand(B, S, -1) if self.config.use_mu_guidance else None
+        plans = self.route_plans(input_ids)
+        new_kvs = [] if use_cache else None
+        n_layers = len(self.layers)
+        normed = rms_norm(h, self.layers[0].input_layernorm.weight, self.layers[0].input_layernorm.eps) \
+            if n_layers else rms_norm(h, self.norm.weight, self.norm.eps)
+        for i, layer in enumerate(self.layers):
+            last = i + 1 == n_layers
+            next_norm = self.norm if last else self.layers[i + 1].input_layernorm
+            h, normed, new_kv, mu = layer.forward_fused(
+                h, normed, next_norm, attention_mask=attention_mask,
+                past_key_value=past_key_values[i] if past_key_values is not None else None,
+                use_cache=use_cache, token_ids=input_ids, mu_prev=mu_prev, route=plans[i],
+                want_mu=not last)
+            if mu is not None:
+                mu_prev = torch.clamp(mu, -2.0, 2.0)
+            if use_cache:
+                new_kvs.append(new_kv)
+        logits = self.lm_head(normed)
+        loss = None
+        if labels is not None:
+            loss = F.cross_entropy(logits[..., :-1, :].contiguous().view(-1, self.config.vocab_size),
+                                   labels[..., 1:].contiguous().view(-1), ignore_index=-100)
+        return CausalLMOutput(loss=loss, logits=logits, past_key_values=new_kvs)
+
+    # ---- generation (modeling.py:225-290) ---------------------------------------
+    @torch.no_grad()
+    def generate(self, input_ids: torch.Tensor, max_new_tokens: int = 100, temperature: float = 1.0,
+                 top_k: int = 50, top_p: float = 0.9, do_sample: bool = True,
+                 eos_token_id: Optional[int] = None) -> torch.Tensor:
+        if eos_token_id is None:
+            eos_token_id = self.config.eos_token_id
+        past = None
+        for _ in range(max_new_tokens):
+            step_ids = input_ids[:, -1:] if past is not None else input_ids
+            out = self.forward(step_ids, past_key_values=past, use_cache=True)
+            past = out.past_key_values
+            logits = out.logits[:, -1, :] / temperature
+            if top_k > 0:
+                kth = torch.topk(logits, top_k)[0][..., -1, None]
+                logits[logits < kth] = float("-inf")
+            if top_p < 1.0:
+                srt, idx = torch.sort(logits, descending=True)
+                cum = torch.cumsum(F.softmax(srt, dim=-1), dim=-1)
+                drop = cum > top_p
+                drop[..., 1:] = drop[..., :-1].clone()
+                drop[..., 0] = False
+                logits[drop.scatter(1, idx, drop)] = float("-inf")
+            if do_sample:
+                nxt = torch.multinomial(F.softmax(logits, dim=-1), num_samples=1)
+            else:
+                nxt = logits.argmax(dim=-1, keepdim=True)
+            input_ids = torch.cat([input_ids, nxt], dim=-1)
+            if (nxt == eos_token_id).all():
+                break
+        return input_ids
+
+    # ---- utilities (modeling.py:296-318) --------------------------------------------
+    def num_parameters(self, trainable_only: bool = True) -> int:
+        return sum(p.numel() for p in self.parameters() if p.requires_grad or not trainable_only)
+
+    def save_pretrained(self, path: str) -> None:
+        p = Path(path)
+        p.mkdir(parents=True, exist_ok=True)
+        with open(p / "config.json", "w") as f:
+            json.dump(self.config.to_dict(), f, indent=2)
+        torch.save(self.state_dict(), p / "model.pt")
+
+    @classmethod
+    def from_pretrained(cls, path: str, device: str = "cpu") -> "ComplexityModel":
+        p = Path(path)
+        with open(p / "config.json") as f:
+            config = ComplexityConfig.from_dict(json.load(f))
+        model = cls(config)
+        weights = torch.load(p / "model.pt", map_location=device, weights_only=True)
+        model.load_state_dict(weights, strict=False)
+        return model.to(device)
+
+
+SIZE_PRESETS = {
+    "tiny": ComplexityConfig.complexity_tiny,
+    "20m": ComplexityConfig.complexity_20m,
+    "small": ComplexityConfig.complexity_small,
+    "150m": ComplexityConfig.complexity_150m,
+    "350m": ComplexityConfig.complexity_350m,
+    "1b": ComplexityConfig.complexity_1b,
+}
+
+
+def create_complexity_model(size: str = "150m", vocab_size: int = 100_000, **overrides) -> ComplexityModel:
+    """Preset config + overrides -> ComplexityModel; models/utils.py:19-44."""
+    if size not in SIZE_PRESETS:
+        raise ValueError(f"Unknown size '{size}'. Choose from {list(SIZE_PRESETS)}")
+    config = SIZE_PRESETS[size]()
+    config.vocab_size = vocab_size
+    for k, v in overrides.items():
+        if hasattr(config, k):
+            setattr(config, k, v)
+    return ComplexityModel(config)
+
+
+def count_parameters(config: ComplexityConfig) -> dict:
+    """Analytic parameter counts; models/utils.py:47-98."""
+    H, I, V, L = config.hidden_size, config.intermediate_size, config.vocab_size, config.num_hidden_layers
+    nq, nkv = config.num_attention_heads, config.num_key_value_heads
+    D = H // nq
+    E = config.num_experts if config.use_token_routed_mlp else 1
+    ie = I // E
+    qkv = nq * D * H + 2 * nkv * D * H
+    attn = qkv + H * H + (qkv if config.use_mu_guidance else 0) + (2 * D if config.use_qk_norm else 0)
+    if config.use_token_routed_mlp:
+        mlp = E * 3 * H * ie + (3 * H * ie if config.shared_expert else 0)
+    else:
+        mlp = 3 * H * I
+    mu = H + H * H if config.use_mu_guidance else 0
+    per_layer = attn + mlp + 2 * H + mu
+    total = V * H + L * per_layer + H
+    return {"total": total, "embedding": V * H, "per_layer": per_layer, "attention_per_layer": attn,
+            "mlp_per_layer": mlp, "mu_per_layer": mu, "num_layers": L,
+            "memory_bf16_gb": total * 2 / (1024 ** 3)}

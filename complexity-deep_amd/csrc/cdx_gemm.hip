@@ -1,0 +1,166 @@
+// C-ABI entry points built on the MFMA tile engine (cdx_gemm.h):
+//   cdx_mu_qkv_fwd       piece 2: one K = 2H contraction over [x | mu_prev]
+//   cdx_moe_swiglu_fwd   piece 1b: gather + gate/up + SwiGLU, then down + scatter,
+//                        with the shared expert folded into both passes
+//   cdx_grouped_gemm_fwd plain grouped GEMM over expert segments
+#include "cdx_gemm.h"
+
+namespace cdx {
+namespace {
+
+template <int BM, int BN, ALoad AL, Epi EP>
+int launch(GemmParams p, hipStream_t s, const char* name) {
+  p.nt_count = (p.N + BN - 1) / BN;
+  const int64_t nb = (int64_t)p.mt_count * p.nt_count;
+  if (nb == 0) return CDX_OK;
+  if (nb > INT32_MAX) return fail(CDX_EUNSUPPORTED, "%s: problem too large (%lld tiles)", name, (long long)nb);
+  gemm_nt_kernel<BM, BN, AL, EP><<<dim3((unsigned)nb), dim3(256), 0, s>>>(p);
+  return check_launch(name);
+}
+
+inline int64_t cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
+
+}  // namespace
+}  // namespace cdx
+
+using cdx::ALoad;
+using cdx::Epi;
+using cdx::GemmParams;
+
+extern "C" int cdx_mu_qkv_fwd(const uint16_t* x, int64_t ldx, const uint16_t* mu, int64_t ldmu,
+                              const uint16_t* w, int64_t ldw, int64_t M, int32_t H, int32_t N,
+                              uint16_t* out, int64_t ldo, void* stream) {
+  using namespace cdx;
+  clear_error();
+  const char* name = "cdx_mu_qkv_fwd";
+  if (M < 0 || H <= 0 || N <= 0) return fail(CDX_EINVAL, "%s: bad shape M=%lld H=%d N=%d", name, (long long)M, H, N);
+  if (H % 64 != 0) return fail(CDX_EUNSUPPORTED, "%s: H=%d must be a multiple of 64", name, H);
+  if (N % 8 != 0) return fail(CDX_EUNSUPPORTED, "%s: N=%d must be a multiple of 8", name, N);
+  const int64_t K = mu ? 2 * (int64_t)H : (int64_t)H;
+  if (ldx < H || ldo < N || ldw < K || (mu && ldmu != 0 && ldmu < H))
+    return fail(CDX_EINVAL, "%s: leading dimension too small", name);
+  if (ldx % 8 || ldo % 8 || ldw % 8 || (mu && ldmu % 8))
+    return fail(CDX_EUNSUPPORTED, "%s: leading dimensions must be multiples of 8", name);
+  if (M == 0) return CDX_OK;
+  if (!x || !w || !out) return fail(CDX_EINVAL, "%s: null pointer", name);
+  if (!aligned16(x) || !aligned16(w) || !aligned16(out) || (mu && !aligned16(mu)))
+    return fail(CDX_EUNSUPPORTED, "%s: pointers must be 16-byte aligned", name);
+  GemmParams p{};
+  p.a = x;
+  p.lda = ldx;
+  p.a2 = mu;
+  p.lda2 = ldmu;
+  p.k_split = H;
+  p.perm = nullptr;
+  p.offsets = nullptr;
+  p.E = 1;
+  p.M = M;
+  p.b = w;
+  p.ldb = ldw;
+  p.b_estride = 0;
+  p.N = N;
+  p.K = (int32_t)K;
+  p.c = out;
+  p.ldc = ldo;
+  constexpr int BM = 256, BN = 256;
+  if (cdiv(M, BM) > INT32_MAX) return fail(CDX_EUNSUPPORTED, "%s: M too large", name);
+  p.mt_count = (int32_t)cdiv(M, BM);
+  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  if (mu) return launch<BM, BN, ALoad::kConcat, Epi::kStore>(p, s, name);
+  return launch<BM, BN, ALoad::kDense, Epi::kStore>(p, s, name);
+}
+
+extern "C" int cdx_moe_swiglu_fwd(const uint16_t* x, int64_t T, int32_t H, int32_t Ie, int32_t E,
+                                  int32_t has_shared, const int32_t* perm, const int32_t* offsets,
+                                  const uint16_t* w_gu, const uint16_t* w_down, uint16_t* inter,
+                                  uint16_t* out, void* stream) {
+  using namespace cdx;
+  clear_error();
+  const char* name = "cdx_moe_swiglu_fwd";
+  if (T < 0 || T > INT32_MAX || H <= 0 || Ie <= 0 || E <= 0 || E > 64)
+    return fail(CDX_EINVAL, "%s: bad shape T=%lld H=%d Ie=%d E=%d", name, (long long)T, H, Ie, E);
+  if (H % 64 != 0) return fail(CDX_EUNSUPPORTED, "%s: H=%d must be a multiple of 64", name, H);
+  if (T == 0) return CDX_OK;
+  if (!x || !perm || !offsets || !w_gu || !w_down || !inter || !out)
+    return fail(CDX_EINVAL, "%s: null pointer", name);
+  if (!aligned16(x) || !aligned16(w_gu) || !aligned16(w_down) || !aligned16(inter) || !aligned16(out))
+    return fail(CDX_EUNSUPPORTED, "%s: pointers must be 16-byte aligned", name);
+  const int32_t P = (Ie + 63) / 64 * 64;
+  const int32_t S = has_shared ? 2 : 1;
+  const int32_t n_gu = 2 * S * P;
+  const int32_t k_down = S * P;
+  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  constexpr int BM = 256, BN = 256;
+  const int32_t mt = (int32_t)(cdiv(T, BM) + E);
+
+  // Pass 1: gathered rows x[perm] times the expert's gate/up rows, SwiGLU epilogue.
+  GemmParams p1{};
+  p1.a = x;
+  p1.lda = H;
+  p1.k_split = H;
+  p1.perm = perm;
+  p1.offsets = offsets;
+  p1.E = E;
+  p1.M = T;
+  p1.b = w_gu;
+  p1.ldb = H;
+  p1.b_estride = (int64_t)n_gu * H;
+  p1.N = n_gu;
+  p1.K = H;
+  p1.c = inter;
+  p1.ldc = k_down;
+  p1.mt_count = mt;
+  if (int rc = launch<BM, BN, ALoad::kGather, Epi::kSwiGLU>(p1, s, name)) return rc;
+
+  // Pass 2: activations (sorted order) times [shared_down | down[e]], rows scattered back.
+  GemmParams p2{};
+  p2.a = inter;
+  p2.lda = k_down;
+  p2.k_split = k_down;
+  p2.perm = perm;
+  p2.offsets = offsets;
+  p2.E = E;
+  p2.M = T;
+  p2.b = w_down;
+  p2.ldb = k_down;
+  p2.b_estride = (int64_t)H * k_down;
+  p2.N = H;
+  p2.K = k_down;
+  p2.c = out;
+  p2.ldc = H;
+  p2.mt_count = mt;
+  return launch<BM, BN, ALoad::kDense, Epi::kScatter>(p2, s, name);
+}
+
+extern "C" int cdx_grouped_gemm_fwd(const uint16_t* a, int64_t T, int32_t K, int32_t N, int32_t E,
+                                    const int32_t* offsets, const uint16_t* w, uint16_t* out,
+                                    void* stream) {
+  using namespace cdx;
+  clear_error();
+  const char* name = "cdx_grouped_gemm_fwd";
+  if (T < 0 || T > INT32_MAX || K <= 0 || N <= 0 || E <= 0 || E > 64)
+    return fail(CDX_EINVAL, "%s: bad shape T=%lld K=%d N=%d E=%d", name, (long long)T, K, N, E);
+  if (K % 64 != 0) return fail(CDX_EUNSUPPORTED, "%s: K=%d must be a multiple of 64", name, K);
+  if (N % 8 != 0) return fail(CDX_EUNSUPPORTED, "%s: N=%d must be a multiple of 8", name, N);
+  if (T == 0) return CDX_OK;
+  if (!a || !offsets || !w || !out) return fail(CDX_EINVAL, "%s: null pointer", name);
+  if (!aligned16(a) || !aligned16(w) || !aligned16(out))
+    return fail(CDX_EUNSUPPORTED, "%s: pointers must be 16-byte aligned", name);
+  GemmParams p{};
+  p.a = a;
+  p.lda = K;
+  p.k_split = K;
+  p.offsets = offsets;
+  p.E = E;
+  p.M = T;
+  p.b = w;
+  p.ldb = K;
+  p.b_estride = (int64_t)N * K;
+  p.N = N;
+  p.K = K;
+  p.c = out;
+  p.ldc = N;
+  constexpr int BM = 256, BN = 256;
+  p.mt_count = (int32_t)(cdiv(T, BM) + E);
+  return launch<BM, BN, ALoad::kDense, Epi::kStore>(p, reinterpret_cast<hipStream_t>(stream), name);
+}

@@ -1,0 +1,178 @@
+/*
+ * cdx.h — C-ABI of the MI355X (gfx950) kernel library for the complexity-deep hot path.
+ *
+ * The library (libcdx.so) holds hand-written HIP kernels for three pieces of the
+ * reference's forward pass:
+ *   1. token-ID-routed MoE: routing plan (lookup, histogram, scan, stable permute)
+ *      and the grouped SwiGLU GEMM with the shared lexical expert folded in;
+ *   2. the mu-guided QKV projection as one contraction over [x | mu_prev];
+ *   3. residual add + RMSNorm.
+ *
+ * Conventions (all entry points):
+ *   - Every pointer argument named *_dev is device memory owned by the caller.
+ *     The library never allocates or frees device memory.
+ *   - `stream` is a hipStream_t passed as void*; all work is enqueued on it and
+ *     nothing synchronises the host.  NULL means the default stream.
+ *   - bf16 tensors are passed as uint16_t* (raw IEEE bfloat16 bits).
+ *   - Return value: 0 on success, a negative CDX_E* code otherwise.  The message
+ *     for the last failure on the calling thread is returned by cdx_last_error().
+ *     Arguments are validated on the host before any launch; an invalid call
+ *     enqueues nothing.
+ *   - Row-major, unit stride in the last dimension; leading dimensions (ld*) are
+ *     in elements.  16-byte alignment is required for every bf16 base pointer and
+ *     leading dimensions must be multiples of 8 elements.
+ *
+ * No entry point has a counterpart in the reference as native code: the reference
+ * hot path is PyTorch/ATen (and unwired Triton).  Each declaration cites the Python
+ * function whose behaviour it replaces.
+ */
+#ifndef CDX_H_
+#define CDX_H_
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ---- status codes --------------------------------------------------------- */
+#define CDX_OK 0
+#define CDX_EINVAL (-1)      /* bad argument: null pointer, negative size, ... */
+#define CDX_EUNSUPPORTED (-2) /* shape or alignment outside what the kernels handle */
+#define CDX_ELAUNCH (-3)     /* the HIP runtime rejected a launch */
+#define CDX_EWORKSPACE (-4)  /* workspace too small */
+
+/* Library version (major*10000 + minor*100 + patch). */
+int cdx_version(void);
+
+/* Message for the last failing call on this host thread ("" if none). */
+const char* cdx_last_error(void);
+
+/* ---- piece 3: residual add + RMSNorm ------------------------------------- */
+
+/*
+ * h   = x + residual                      (rounded to bf16, written to residual_out)
+ * out = weight * h * rsqrt(mean(h^2) + eps)   (fp32 math, rounded once to bf16)
+ *
+ * residual == NULL  -> plain RMSNorm of x (residual_out must then be NULL).
+ * residual_out may alias residual (in-place update) or x.
+ * Shapes: x, residual, out, residual_out [T, H] contiguous; weight [H].
+ * H must be a multiple of 8 and at most 8192.
+ *
+ * Replaces: core/normalization.py:29-32 (RMSNorm.forward), core/layer.py:174,183
+ * (residual adds), cuda/fused_residual.py:333-399 (fused_residual_rmsnorm) and
+ * cuda/fused_residual.py:478-533 (fused_add_rmsnorm_inplace).
+ */
+int cdx_add_rmsnorm_fwd(const uint16_t* x_dev, const uint16_t* residual_dev,
+                        const uint16_t* weight_dev, float eps, int64_t T, int32_t H,
+                        uint16_t* out_dev, uint16_t* residual_out_dev, void* stream);
+
+/* ---- piece 1a: routing plan ------------------------------------------------ */
+
+/* Bytes of workspace cdx_route_plan needs for T tokens and E experts. */
+size_t cdx_route_workspace_bytes(int64_t T, int32_t E);
+
+/*
+ * expert_id[t] = map[clamp(ids[t], 0, V-1)]        (map == NULL: expert_id[t] = ids[t])
+ * counts[e]    = #{t : expert_id[t] == e}
+ * offsets      = [0, counts[0], counts[0]+counts[1], ...]   (E+1 entries)
+ * perm         = stable argsort of expert_id (sorted position -> token index)
+ * inv_perm     = inverse of perm                  (token index -> sorted position)
+ *
+ * All outputs are int32 and bit-exact against a stable counting sort.  E <= 64.
+ * Expert ids outside [0, E) (possible only through a corrupt map or map == NULL)
+ * are clamped into range so that no access leaves its buffer.
+ * T == 0 is valid (counts and offsets are zeroed).
+ *
+ * Replaces: core/token_routed_mlp.py:149-150 (lookup), :166-170 (mask dispatch),
+ * cuda/triton_token_routed.py:37-61 (sort_tokens_by_expert: sort, bincount, cumsum).
+ */
+int cdx_route_plan(const int64_t* ids_dev, int64_t T, const int64_t* map_dev, int64_t V,
+                   int32_t E, int32_t* expert_id_dev, int32_t* perm_dev,
+                   int32_t* inv_perm_dev, int32_t* counts_dev, int32_t* offsets_dev,
+                   void* workspace_dev, size_t workspace_bytes, void* stream);
+
+/*
+ * Row gather / scatter by a permutation (rows of `row_bytes` bytes, a multiple of 16):
+ *   permute:    out[i]       = in[perm[i]]
+ *   unpermute:  out[perm[i]] = in[i]
+ * Replaces: cuda/triton_token_routed.py:55 (tokens[sorted_indices]) and
+ * :385-386 (output[sorted_indices] = sorted_output); core/token_routed_mlp.py:170,174.
+ */
+int cdx_permute_rows(const void* in_dev, const int32_t* perm_dev, int64_t T,
+                     int64_t row_bytes, void* out_dev, void* stream);
+int cdx_unpermute_rows(const void* in_dev, const int32_t* perm_dev, int64_t T,
+                       int64_t row_bytes, void* out_dev, void* stream);
+
+/* ---- piece 1b: token-routed SwiGLU MoE ------------------------------------ */
+
+/*
+ * Packed weight layouts (bf16, K-contiguous, built once by the caller):
+ *   P   = round_up(Ie, 32)                  padded expert width
+ *   S   = has_shared ? 2 : 1                number of SwiGLU blocks per token
+ *   w_gu   [E][S*2*P][H]   gate/up rows for the shared block (if any) then the routed
+ *                          block; inside a block, rows come in groups of 64:
+ *                          32 gate rows (intermediate cols j..j+31) then the 32 up rows
+ *                          for the same cols.  Padding rows are zero.
+ *   w_down [E][H][S*P]     row n = output feature n; cols [0,P) shared down weights
+ *                          (if any), then the routed expert's down weights.  Padding
+ *                          cols are zero.
+ *   The shared block is replicated into each expert's slice (it is 1/S of the slice).
+ *
+ * Computes, for every token t with e = expert_id[t]:
+ *   a_s = silu(x_t Wsg^T) * (x_t Wsu^T)          (if has_shared)
+ *   a_r = silu(x_t Wg[e]) * (x_t Wu[e])
+ *   out_t = a_s Wsd^T + a_r Wd[e]                 (one fp32 accumulation, one rounding)
+ * `inter_dev` is a caller workspace of [T, S*P] bf16 holding the activations in
+ * sorted (perm) order.  x and out are [T, H] in original token order.
+ * perm/offsets come from cdx_route_plan (offsets is [E+1] int32 on the device).
+ * H must be a multiple of 64.
+ *
+ * Replaces: core/token_routed_mlp.py:157-178 (shared expert, per-expert loop,
+ * combine), cuda/triton_token_routed.py:339-388 (_cggr_forward),
+ * cuda/persistent_cggr.py:479-530 (persistent_swiglu_cggr).
+ */
+int cdx_moe_swiglu_fwd(const uint16_t* x_dev, int64_t T, int32_t H, int32_t Ie, int32_t E,
+                       int32_t has_shared, const int32_t* perm_dev,
+                       const int32_t* offsets_dev, const uint16_t* w_gu_dev,
+                       const uint16_t* w_down_dev, uint16_t* inter_dev, uint16_t* out_dev,
+                       void* stream);
+
+/*
+ * Grouped GEMM over expert segments of an already sorted token matrix:
+ *   out[offsets[e]:offsets[e+1], :] = a[offsets[e]:offsets[e+1], :] @ W[e]
+ * with W given K-contiguous: w_dev is [E][N][K] (W[e] transposed).  K % 64 == 0.
+ * Replaces: cuda/triton_token_routed.py:197-231 (cggr_grouped_gemm_triton) and
+ * :64-86 (grouped_gemm_pytorch).
+ */
+int cdx_grouped_gemm_fwd(const uint16_t* a_dev, int64_t T, int32_t K, int32_t N, int32_t E,
+                         const int32_t* offsets_dev, const uint16_t* w_dev,
+                         uint16_t* out_dev, void* stream);
+
+/* ---- piece 2: mu-guided QKV projection ------------------------------------- */
+
+/*
+ * out[M, N] = [x | mu] @ w_pack^T, one K = 2H contraction, fp32 accumulate.
+ *   x      [M, H]  leading dim ldx
+ *   mu     [M, H]  leading dim ldmu; ldmu == 0 broadcasts one row (layer 0's
+ *                  mu_init.expand); mu == NULL means no mu term (K = H)
+ *   w_pack [N, 2H] rows = output features, cols [0,H) the x weights
+ *                  (q_proj|k_proj|v_proj rows stacked) and [H,2H) the mu weights
+ *                  (mu_to_q|mu_to_k|mu_to_v).  With mu == NULL, w_pack is [N, H]
+ *                  with leading dim ldw (ldw >= H).
+ *   out    [M, N]  leading dim ldo; q = cols [0, Nq*D), k, v follow.
+ * H % 64 == 0.
+ *
+ * Replaces: core/attention.py:120-131 (cat + three F.linear),
+ * cuda/triton_mu_qkv.py:195-283 (fused_mu_qkv_projection).
+ */
+int cdx_mu_qkv_fwd(const uint16_t* x_dev, int64_t ldx, const uint16_t* mu_dev, int64_t ldmu,
+                   const uint16_t* w_pack_dev, int64_t ldw, int64_t M, int32_t H, int32_t N,
+                   uint16_t* out_dev, int64_t ldo, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* CDX_H_ */

@@ -1,0 +1,121 @@
+"""CPU checks of the C-ABI boundary (no kernel is launched).
+
+* libcdx.so loads and exports every function declared in include/cdx.h, and the
+  ctypes table in complexity_deep/_native.py binds exactly that set.
+* Host-side argument validation rejects bad calls with the documented status codes
+  and a message, before anything is enqueued (so these run without a GPU).
+* The product fails loudly instead of falling back: CPU tensors and a missing
+  library raise.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import re
+from pathlib import Path
+
+import pytest
+import torch
+
+REPO = Path(__file__).resolve().parents[1]
+HEADER = REPO / "include" / "cdx.h"
+
+CDX_EINVAL, CDX_EUNSUPPORTED, CDX_EWORKSPACE = -1, -2, -4
+
+
+def _declared():
+    text = re.sub(r"/\*.*?\*/", "", HEADER.read_text(), flags=re.S)
+    return sorted(set(re.findall(r"\b(cdx_[a-z0-9_]+)\s*\(", text)))
+
+
+@pytest.fixture(scope="module")
+def lib():
+    from complexity_deep import _native
+    if not _native.LIB_PATH.exists():
+        import importlib.util
+        spec = importlib.util.spec_from_file_location("build_native", REPO / "complexity-deep_amd" / "build_native.py")
+        mod = importlib.util.module_from_spec(spec)
+        spec.loader.exec_module(mod)
+        mod.build()
+    return _native.lib()
+
+
+def test_header_symbols_exported(lib):
+    from complexity_deep import _native
+    names = _declared()
+    assert len(names) >= 10
+    for n in names:
+        assert hasattr(lib, n), f"{n} declared in cdx.h but not exported"
+    assert sorted(_native.exported_symbols()) == names
+
+
+def test_version_and_error_string(lib):
+    assert lib.cdx_version() >= 100
+    assert isinstance(lib.cdx_last_error(), bytes)
+
+
+def test_norm_validation(lib):
+    rc = lib.cdx_add_rmsnorm_fwd(16, None, 16, 1e-6, 4, 7, 16, None, None)
+    assert rc == CDX_EUNSUPPORTED and b"multiple of 8" in lib.cdx_last_error()
+    assert lib.cdx_add_rmsnorm_fwd(16, None, 16, 1e-6, -1, 8, 16, None, None) == CDX_EINVAL
+    assert lib.cdx_add_rmsnorm_fwd(None, None, None, 1e-6, 4, 8, None, None, None) == CDX_EINVAL
+    assert lib.cdx_add_rmsnorm_fwd(16, None, 16, -1.0, 4, 8, 16, None, None) == CDX_EINVAL
+    assert lib.cdx_add_rmsnorm_fwd(16, None, 16, 1e-6, 4, 8, 16, 32, None) == CDX_EINVAL  # residual_out w/o residual
+    assert lib.cdx_add_rmsnorm_fwd(18, None, 16, 1e-6, 4, 8, 16, None, None) == CDX_EUNSUPPORTED  # misaligned
+    assert lib.cdx_add_rmsnorm_fwd(None, None, None, 1e-6, 0, 8, None, None, None) == 0  # T == 0 is a no-op
+
+
+def test_route_validation(lib):
+    assert lib.cdx_route_workspace_bytes(0, 4) == 0
+    assert lib.cdx_route_workspace_bytes(1024, 4) == 2 * 1 * 4 * 4
+    assert lib.cdx_route_workspace_bytes(1025, 8) == 2 * 2 * 8 * 4
+    assert lib.cdx_route_plan(16, 10, 16, 5, 65, 16, 16, 16, 16, 16, 16, 1 << 20, None) == CDX_EUNSUPPORTED
+    assert lib.cdx_route_plan(16, 10, 16, 0, 4, 16, 16, 16, 16, 16, 16, 1 << 20, None) == CDX_EINVAL
+    assert lib.cdx_route_plan(16, 2048, 16, 5, 4, 16, 16, 16, 16, 16, 16, 8, None) == CDX_EWORKSPACE
+    assert lib.cdx_route_plan(16, -1, 16, 5, 4, 16, 16, 16, 16, 16, 16, 0, None) == CDX_EINVAL
+    assert lib.cdx_route_plan(None, 10, 16, 5, 4, 16, 16, 16, 16, 16, 16, 1 << 20, None) == CDX_EINVAL
+    assert lib.cdx_permute_rows(16, 16, 4, 24, 16, None) == CDX_EUNSUPPORTED
+    assert lib.cdx_unpermute_rows(None, None, 0, 32, None, None) == 0
+
+
+def test_gemm_validation(lib):
+    assert lib.cdx_mu_qkv_fwd(16, 96, 16, 96, 16, 192, 8, 96, 64, 16, 64, None) == CDX_EUNSUPPORTED  # H % 64
+    assert lib.cdx_mu_qkv_fwd(16, 64, 16, 64, 16, 128, 8, 64, 60, 16, 64, None) == CDX_EUNSUPPORTED  # N % 8
+    assert lib.cdx_mu_qkv_fwd(16, 32, 16, 64, 16, 128, 8, 64, 64, 16, 64, None) == CDX_EINVAL  # ldx < H
+    assert lib.cdx_mu_qkv_fwd(16, 64, 16, 64, 16, 64, 8, 64, 64, 16, 64, None) == CDX_EINVAL  # ldw < 2H with mu
+    assert lib.cdx_moe_swiglu_fwd(16, 8, 96, 64, 4, 1, 16, 16, 16, 16, 16, 16, None) == CDX_EUNSUPPORTED
+    assert lib.cdx_moe_swiglu_fwd(16, 8, 64, 64, 65, 1, 16, 16, 16, 16, 16, 16, None) == CDX_EINVAL
+    assert lib.cdx_moe_swiglu_fwd(None, 0, 64, 64, 4, 1, None, None, None, None, None, None, None) == 0
+    assert lib.cdx_grouped_gemm_fwd(16, 8, 48, 64, 4, 16, 16, 16, None) == CDX_EUNSUPPORTED
+    assert b"multiple of 64" in lib.cdx_last_error()
+
+
+def test_cpu_tensors_raise():
+    from complexity_deep.normalization import add_rms_norm
+    x = torch.randn(4, 64, dtype=torch.bfloat16)
+    with pytest.raises(RuntimeError, match="ROCm GPU"):
+        add_rms_norm(x, None, torch.ones(64, dtype=torch.bfloat16))
+
+
+def test_missing_library_raises(monkeypatch, tmp_path):
+    from complexity_deep import _native
+    monkeypatch.setattr(_native, "_lib", None)
+    monkeypatch.setattr(_native, "LIB_PATH", tmp_path / "libcdx.so")
+    with pytest.raises(_native.NativeLibraryMissing):
+        _native.lib()
+
+
+def test_forward_only_guard():
+    from complexity_deep import ComplexityConfig, ComplexityModel
+    cfg = ComplexityConfig(vocab_size=64, hidden_size=64, intermediate_size=128, num_hidden_layers=1,
+                           num_attention_heads=2, num_key_value_heads=1)
+    m = ComplexityModel(cfg)
+    with pytest.raises(NotImplementedError, match="forward-only"):
+        m(torch.zeros(1, 4, dtype=torch.long))
+
+
+def test_ctypes_only_plain_types():
+    from complexity_deep import _native
+    for name, (res, args) in _native._SIGNATURES.items():
+        for a in args:
+            assert a in (ctypes.c_void_p, ctypes.c_int64, ctypes.c_int32, ctypes.c_float, ctypes.c_size_t), name

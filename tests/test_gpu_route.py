@@ -1,0 +1,89 @@
+"""GPU routing plan (cdx_route_plan) and row permutes: bit-exact against the C oracle.
+
+Covers the token streams of configurations 1, 2, 4 and 5 (Zipf(1.1) ids with the
+bin-packed map; the 90%-skew stress stream), block boundaries (1023/1024/1025
+tokens), T = 0 and 1, E = 1 and 64, out-of-range ids (clamped) and expert ids given
+directly (map = NULL, the sort_tokens_by_expert path).
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+pytestmark = pytest.mark.gpu
+
+
+def _check(plan, ref):
+    for k in ("expert_id", "perm", "inv_perm", "counts", "offsets"):
+        got = getattr(plan, k).cpu().numpy().astype(np.int64)
+        np.testing.assert_array_equal(got, ref[k].astype(np.int64), err_msg=k)
+
+
+def _zipf_case(cfg):
+    from complexity_deep import synthetic as syn
+    name, B, S, E, seed = cfg
+    ids = syn.zipf_token_ids(B, S, 32000, seed=seed)
+    tmap = syn.binpacked_map(32000, E)
+    return ids, tmap
+
+
+@pytest.mark.parametrize("cfg", [("cfg1", 4, 512, 4, 0), ("cfg2", 1, 16384, 4, 0), ("cfg4", 8, 2048, 8, 1)])
+def test_plan_zipf_configs(cdx, oracle, cfg):
+    print(f"route plan {cfg}", flush=True)
+    ids, tmap = _zipf_case(cfg)
+    E = cfg[3]
+    plan = cdx.route_plan(ids.cuda(), tmap.cuda(), E)
+    _check(plan, oracle.route_plan(ids.numpy(), tmap.numpy(), E))
+
+
+def test_plan_stress_cfg5(cdx, oracle):
+    from complexity_deep import synthetic as syn
+    print("route plan cfg5 stress", flush=True)
+    tmap = syn.binpacked_map(32000, 8)
+    ids = syn.routing_stress_ids(65536, tmap, 8, heavy=1, seed=0)
+    plan = cdx.route_plan(ids.cuda(), tmap.cuda(), 8)
+    ref = oracle.route_plan(ids.numpy(), tmap.numpy(), 8)
+    _check(plan, ref)
+    assert int(plan.counts[1]) == round(0.9 * 65536)
+
+
+@pytest.mark.parametrize("T,V,E,seed", [(0, 10, 4, 0), (1, 10, 4, 1), (1023, 300, 4, 2), (1024, 300, 4, 3),
+                                        (1025, 300, 8, 4), (4097, 50, 1, 5), (3000, 5000, 64, 6),
+                                        (100000, 32000, 8, 7)])
+def test_plan_edge_cases(cdx, oracle, T, V, E, seed):
+    print(f"route plan T={T} V={V} E={E}", flush=True)
+    rng = np.random.default_rng(seed)
+    ids = rng.integers(-7, V + 7, size=T).astype(np.int64)
+    tmap = rng.integers(0, E, size=V).astype(np.int64)
+    plan = cdx.route_plan(torch.from_numpy(ids).cuda(), torch.from_numpy(tmap).cuda(), E)
+    _check(plan, oracle.route_plan(ids, tmap, E))
+
+
+def test_plan_direct_expert_ids(cdx, oracle):
+    rng = np.random.default_rng(8)
+    eids = rng.integers(0, 5, size=7777).astype(np.int64)
+    plan = cdx.route_plan(torch.from_numpy(eids).cuda(), None, 5)
+    _check(plan, oracle.route_plan(eids, None, 5))
+
+
+def test_permute_roundtrip_and_sort_api(cdx, oracle):
+    from complexity_deep.token_routed_mlp import permute_rows, unpermute_rows
+    print("permute/unpermute + sort_tokens_by_expert", flush=True)
+    rng = np.random.default_rng(9)
+    T, H, E = 5000, 2048, 8
+    eids = rng.integers(0, E, size=T).astype(np.int64)
+    x = torch.randn(T, H).to(torch.bfloat16).cuda()
+    e_dev = torch.from_numpy(eids).cuda()
+    sorted_x, sorted_idx, offs, counts = cdx.sort_tokens_by_expert(x, e_dev, E)
+    ref = oracle.route_plan(eids, None, E)
+    assert sorted_idx.dtype == torch.int64 and offs.dtype == torch.int64 and counts.dtype == torch.int64
+    np.testing.assert_array_equal(sorted_idx.cpu().numpy(), ref["perm"])
+    np.testing.assert_array_equal(offs.cpu().numpy(), ref["offsets"])
+    np.testing.assert_array_equal(counts.cpu().numpy(), ref["counts"])
+    assert torch.equal(sorted_x, x[sorted_idx])
+    perm = sorted_idx.to(torch.int32)
+    back = unpermute_rows(sorted_x, perm)
+    assert torch.equal(back, x)
+    assert torch.equal(permute_rows(x, perm), sorted_x)
