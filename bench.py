@@ -1,0 +1,357 @@
+#!/usr/bin/env python3
+"""Benchmark of the complexity-deep hot path on one MI355X.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload NAME] [--no-cpu-baseline]
+
+Default workload ("1b-forward", configuration 4): one full ComplexityModel forward of
+the 1B preset (hidden 2048, 24 layers, 16 Q / 8 KV heads, intermediate 5632, 8 routed
+experts + shared expert, vocab 32000) in bf16 over batch 8 x seq 2048 token ids drawn
+from Zipf(1.1), with the greedy bin-packed expert map installed in every layer and
+random-normal weights (seed 1).  A step is one forward returning logits; `value` is
+tokens per second with inputs already in HBM.
+
+The other workloads run one hot-path piece on its own (for profiling):
+  "moe-layer"     configuration 2: TokenRoutedMLP, 16384 x 768, E=4, Ie=512 + shared
+  "qkv-norm"      configuration 3: add+RMSNorm then mu-QKV, 32768 x 2048, 16q/8kv x 128
+  "route-stress"  configuration 5: routing plan + MoE layer, 65536 tokens, 90% skew
+
+Printed: ONE JSON line on stdout.  Besides the contract keys it carries
+  roofline      the dominant hot-path kernel's achieved rate against the MI355X peak
+                (2.5 PFLOP/s dense bf16 MFMA, 8 TB/s HBM), from HIP events recorded
+                around each launch on the stream it runs on, over the timed steps;
+  kernels       the same for every hot-path entry point;
+  cpu_baseline  the fp32 CPU restatement (oracle/) timed on this host over a bounded
+                sample of the same workload, plus its agreement with the GPU logits.
+Everything else goes to stderr.
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import platform
+import sys
+import time
+from collections import defaultdict
+from pathlib import Path
+
+REPO = Path(__file__).resolve().parent
+for _p in (REPO, REPO / "complexity-deep_amd"):
+    if str(_p) not in sys.path:
+        sys.path.insert(0, str(_p))
+
+PEAK_BF16_TFLOPS = 2500.0   # MI355X dense bf16 MFMA
+PEAK_HBM_GBS = 8000.0       # MI355X HBM3E
+
+METRIC = "fwd tokens/sec at 1B bf16; MFMA util % (MoE/QKV GEMM), HBM % (route/norm)"
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+# ---------------------------------------------------------------------------
+# algorithmic work per entry-point call (the units roofline.achieved is priced on)
+# ---------------------------------------------------------------------------
+
+def work_of(name: str, s: dict):
+    """(amount, kind) per call: FLOP for MFMA-bound calls, bytes for HBM-bound ones."""
+    if name == "mu_qkv":
+        K = 2 * s["H"] if s["mu"] else s["H"]
+        return 2.0 * s["M"] * K * s["N"], "flop"
+    if name == "moe_swiglu":
+        blocks = 2 if s["shared"] else 1
+        # gate + up + down per block, each token sees one routed expert (+ shared)
+        return 6.0 * s["T"] * s["H"] * s["Ie"] * blocks, "flop"
+    if name == "add_rmsnorm":
+        rows = s["T"] * s["H"] * 2
+        return float(rows * (4 if s["store_residual"] else 3) + 2 * s["H"]), "byte"
+    if name == "rmsnorm":
+        return float(2 * s["T"] * s["H"] * 2 + 2 * s["H"]), "byte"
+    if name == "route_plan":
+        # ids in; expert_id, perm, inv_perm out; the map is read once per token at most
+        return float(s["T"] * (8 + 4 + 4 + 4) + 2 * 4 * (s["E"] + 1)), "byte"
+    return 0.0, "none"
+
+
+class KernelTimer:
+    """Collects (name, start, end, shape) from the package's launch hook."""
+
+    def __init__(self):
+        self.events = []
+        self.active = False
+
+    def __call__(self, name, e0, e1, shape):
+        if self.active:
+            self.events.append((name, e0, e1, shape))
+
+    def summary(self, steps: int):
+        import torch
+        torch.cuda.synchronize()
+        acc = defaultdict(lambda: {"calls": 0, "ms": 0.0, "work": 0.0, "kind": "none"})
+        for name, e0, e1, shape in self.events:
+            a = acc[name]
+            a["calls"] += 1
+            a["ms"] += e0.elapsed_time(e1)
+            w, kind = work_of(name, shape)
+            a["work"] += w
+            a["kind"] = kind
+        out = {}
+        for name, a in acc.items():
+            avg_us = 1e3 * a["ms"] / a["calls"]
+            rec = {"launches_per_step": a["calls"] / steps, "avg_us": round(avg_us, 2),
+                   "ms_per_step": round(a["ms"] / steps, 4)}
+            if a["kind"] == "flop":
+                tf = a["work"] / (a["ms"] * 1e-3) / 1e12
+                rec.update(bound="mfma", achieved=round(tf, 1), unit="TFLOP/s",
+                           frac=round(tf / PEAK_BF16_TFLOPS, 4), work_per_launch=a["work"] / a["calls"])
+            elif a["kind"] == "byte":
+                gbs = a["work"] / (a["ms"] * 1e-3) / 1e9
+                rec.update(bound="hbm", achieved=round(gbs, 1), unit="GB/s",
+                           frac=round(gbs / PEAK_HBM_GBS, 4), work_per_launch=a["work"] / a["calls"])
+            out[name] = rec
+        return out
+
+
+# ---------------------------------------------------------------------------
+# workloads
+# ---------------------------------------------------------------------------
+
+def build_1b(dev):
+    import torch
+    import complexity_deep as cd
+    from complexity_deep import synthetic as syn
+    cfg = cd.ComplexityConfig.complexity_1b()
+    cfg.vocab_size = 32000
+    torch.manual_seed(1)
+    with torch.device(dev):
+        model = cd.ComplexityModel(cfg)
+    tmap = syn.binpacked_map(cfg.vocab_size, cfg.num_experts)
+    syn.install_expert_map(model, tmap)
+    model = model.to(torch.bfloat16).eval()
+    ids = syn.zipf_token_ids(8, 2048, cfg.vocab_size, seed=1)
+    return cfg, model, ids
+
+
+def workload_1b(args, dev):
+    import torch
+    cfg, model, ids_cpu = build_1b(dev)
+    ids = ids_cpu.to(dev)
+    T = ids.numel()
+
+    def step():
+        return model(ids).logits
+
+    config = {"workload": "configuration 4: 1B ComplexityModel forward (logits)", "preset": "complexity_1b",
+              "hidden": cfg.hidden_size, "layers": cfg.num_hidden_layers,
+              "heads_q_kv_dim": [cfg.num_attention_heads, cfg.num_key_value_heads,
+                                 cfg.hidden_size // cfg.num_attention_heads],
+              "intermediate": cfg.intermediate_size, "experts": cfg.num_experts,
+              "expert_width": cfg.intermediate_size // cfg.num_experts, "shared_expert": True,
+              "vocab": cfg.vocab_size, "global_batch": 8, "seq_len": 2048, "tokens_per_step": T,
+              "token_ids": "Zipf(1.1) over 32000, seed 1", "expert_map": "greedy bin-packing of the Zipf pmf",
+              "weights": "random normal init (std 0.02, residual 0.02/sqrt(48)), seed 1, cast to bf16",
+              "parallelism": "single GPU"}
+    return step, T, config, ("mu_qkv",), (cfg, model, ids_cpu)
+
+
+def workload_moe(args, dev):
+    import torch
+    import complexity_deep as cd
+    from complexity_deep import synthetic as syn
+    T, H, I, E = 16384, 768, 2048, 4
+    torch.manual_seed(0)
+    with torch.device(dev):
+        m = cd.TokenRoutedMLP(H, I, num_experts=E, vocab_size=32000)
+        m.token_to_expert.copy_(syn.binpacked_map(32000, E))
+    m = m.to(torch.bfloat16)
+    ids = syn.zipf_token_ids(1, T, 32000, seed=0).to(dev)
+    x = syn.normal_bf16((1, T, H), seed=1, device=dev)
+
+    def step():
+        return m(x, token_ids=ids)
+
+    config = {"workload": "configuration 2: one TokenRoutedMLP layer (route plan + grouped SwiGLU + shared)",
+              "tokens_per_step": T, "hidden": H, "experts": E, "expert_width": I // E, "shared_expert": True,
+              "token_ids": "Zipf(1.1) over 32000, seed 0", "expert_map": "greedy bin-packing"}
+    return step, T, config, ("moe_swiglu",), None
+
+
+def workload_qkv_norm(args, dev):
+    import torch
+    import complexity_deep as cd
+    from complexity_deep import synthetic as syn
+    from complexity_deep.normalization import add_rms_norm
+    B, S, H, nq, nkv = 16, 2048, 2048, 16, 8
+    torch.manual_seed(0)
+    with torch.device(dev):
+        attn = cd.ComplexityAttention(H, nq, nkv)
+        w = torch.ones(H)
+    attn = attn.to(torch.bfloat16)
+    w = w.to(torch.bfloat16)
+    x = syn.normal_bf16((B, S, H), seed=1, device=dev)
+    res = syn.normal_bf16((B, S, H), seed=2, device=dev)
+    mu = syn.normal_bf16((B, S, H), seed=3, device=dev)
+    h = torch.empty_like(res)
+
+    def step():
+        n, _ = add_rms_norm(x, res, w, 1e-6, residual_out=h)
+        return attn.project_qkv(n, mu)
+
+    config = {"workload": "configuration 3: residual add + RMSNorm, then the mu-QKV projection",
+              "tokens_per_step": B * S, "hidden": H, "heads_q_kv_dim": [nq, nkv, H // nq], "eps": 1e-6}
+    return step, B * S, config, ("mu_qkv", "add_rmsnorm"), None
+
+
+def workload_route_stress(args, dev):
+    import torch
+    import complexity_deep as cd
+    from complexity_deep import synthetic as syn
+    T, H, I, E = 65536, 2048, 5632, 8
+    tmap = syn.binpacked_map(32000, E)
+    torch.manual_seed(0)
+    with torch.device(dev):
+        m = cd.TokenRoutedMLP(H, I, num_experts=E, vocab_size=32000)
+        m.token_to_expert.copy_(tmap)
+    m = m.to(torch.bfloat16)
+    ids = syn.routing_stress_ids(T, tmap, E, heavy=1, seed=0).to(dev)
+    x = syn.normal_bf16((T, H), seed=2, device=dev)
+
+    def step():
+        return m(x, token_ids=ids)
+
+    config = {"workload": "configuration 5: routing plan + MoE layer under 90% skew", "tokens_per_step": T,
+              "hidden": H, "experts": E, "expert_width": I // E,
+              "token_ids": "90% heavy expert 1, 1% each other, rest id 0, seed 0"}
+    return step, T, config, ("moe_swiglu", "route_plan"), None
+
+
+WORKLOADS = {"1b-forward": workload_1b, "moe-layer": workload_moe, "qkv-norm": workload_qkv_norm,
+             "route-stress": workload_route_stress}
+
+
+# ---------------------------------------------------------------------------
+# CPU baseline: the fp32 oracle on this host's cores, bounded sample
+# ---------------------------------------------------------------------------
+
+def cpu_model_name() -> str:
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return platform.processor() or "unknown"
+
+
+def cpu_baseline_1b(ctx, gpu_logits0, seqs: int):
+    import torch
+    from oracle import oracle as orc
+    cfg, model, ids_cpu = ctx
+    log("cpu baseline: copying weights to host fp32")
+    sd = {k: v.detach().float().cpu() for k, v in model.state_dict().items()}
+    sample = ids_cpu[:seqs]
+    threads = torch.get_num_threads()
+    with torch.no_grad():
+        orc.forward(sd, cfg.to_dict(), sample[:, :64])  # warm-up (allocator, BLAS threads)
+        t0 = time.perf_counter()
+        ref = orc.forward(sd, cfg.to_dict(), sample)
+        dt = time.perf_counter() - t0
+    tok = sample.numel()
+    d = gpu_logits0[:seqs].float().cpu() - ref
+    max_rel = float(d.abs().max() / ref.abs().max())
+    rel_rms = float(d.pow(2).mean().sqrt() / ref.pow(2).mean().sqrt())
+    log(f"cpu baseline: {tok} tokens in {dt:.2f} s ({tok / dt:.1f} tok/s, {threads} threads); "
+        f"GPU logits vs CPU fp32: max_rel={max_rel:.3e} rel_rms={rel_rms:.3e}")
+    return {"value": round(tok / dt, 2), "unit": "tokens/s", "cores": threads, "kind": "port",
+            "sample": f"{seqs} x 2048 tokens (the first {seqs} sequence(s) of the workload batch), the full "
+                      f"24-layer 1B forward in fp32 through oracle.forward (torch CPU, {threads} threads)",
+            "seconds": round(dt, 3), "cpu_model": cpu_model_name(), "affinity_cores": len(os.sched_getaffinity(0)),
+            "gpu_vs_cpu_logits": {"max_rel": max_rel, "rel_rms": rel_rms}}
+
+
+# ---------------------------------------------------------------------------
+
+def main() -> int:
+    ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=10)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--workload", choices=sorted(WORKLOADS), default="1b-forward")
+    ap.add_argument("--no-cpu-baseline", action="store_true", help="skip the CPU oracle timing")
+    ap.add_argument("--cpu-seqs", type=int, default=1, help="sequences of 2048 tokens in the CPU sample")
+    ap.add_argument("--no-kernel-timing", action="store_true", help="do not record per-launch events")
+    args = ap.parse_args()
+
+    world = int(os.environ.get("WORLD_SIZE", "1"))
+    if args.gpus != 1 or world != 1:
+        print(f"bench.py: this build measures one GPU only (asked for --gpus {args.gpus}, WORLD_SIZE {world}); "
+              "the multi-GPU sharding of this path is a design, not a measured configuration", file=sys.stderr)
+        return 2
+
+    import torch
+    from complexity_deep import _native as nat
+    if not torch.cuda.is_available():
+        log("bench.py needs a ROCm GPU")
+        return 1
+    nat.lib()
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    log(f"device: {torch.cuda.get_device_name(dev)}; workload {args.workload}")
+    step, tokens, config, dominant, ctx = WORKLOADS[args.workload](args, dev)
+
+    timer = KernelTimer()
+    if not args.no_kernel_timing:
+        nat.set_launch_hook(timer)
+    with torch.inference_mode():
+        for i in range(args.warmup):
+            out = step()
+        torch.cuda.synchronize()
+        log(f"warm-up done ({args.warmup} steps)")
+        timer.active = True
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(args.steps):
+            out = step()
+        torch.cuda.synchronize()
+        t1 = time.perf_counter()
+        timer.active = False
+    nat.set_launch_hook(None)
+    elapsed = t1 - t0
+    ms = 1e3 * elapsed / args.steps
+    value = tokens * args.steps / elapsed
+    log(f"timed {args.steps} steps: {ms:.3f} ms/step, {value:.1f} tokens/s")
+
+    kernels = timer.summary(args.steps) if not args.no_kernel_timing else {}
+    hot_ms = sum(k["ms_per_step"] for k in kernels.values())
+    for name, k in sorted(kernels.items()):
+        log(f"  {name:12s} {k['launches_per_step']:5.1f}/step avg {k['avg_us']:9.2f} us  "
+            f"{k.get('achieved', 0):9.1f} {k.get('unit', '')}  frac {k.get('frac', 0):.3f}")
+    roofline = None
+    dom = next((d for d in dominant if d in kernels), None)
+    if dom is not None:
+        k = kernels[dom]
+        roofline = {"kernel": dom, "bound": k["bound"], "achieved": k["achieved"],
+                    "peak": PEAK_BF16_TFLOPS if k["bound"] == "mfma" else PEAK_HBM_GBS,
+                    "unit": k["unit"], "frac": k["frac"], "traffic": None,
+                    "work_per_launch": k["work_per_launch"], "avg_launch_us": k["avg_us"],
+                    "timing": "HIP events around each launch on its stream, over the timed steps"}
+
+    cpu = None
+    if args.workload == "1b-forward" and not args.no_cpu_baseline:
+        cpu = cpu_baseline_1b(ctx, out, args.cpu_seqs)
+
+    rec = {"metric": METRIC, "value": round(value, 1), "unit": "tokens/s", "n_gpus": 1, "steps": args.steps,
+           "warmup": args.warmup, "ms_per_step": round(ms, 4), "higher_is_better": True, "scaling": "weak",
+           "vs_baseline": None, "dtype": "bf16", "data": "synthetic", "config": config,
+           "roofline": roofline, "cpu_baseline": cpu,
+           "kernels": kernels, "hot_path_ms_per_step": round(hot_ms, 4),
+           "device": torch.cuda.get_device_name(dev)}
+    print(json.dumps(rec), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

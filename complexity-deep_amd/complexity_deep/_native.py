@@ -8,9 +8,10 @@ stream and nothing synchronises the host.
 
 from __future__ import annotations
 
+import contextlib
 import ctypes
 from pathlib import Path
-from typing import Optional
+from typing import Callable, Optional
 
 import torch
 
@@ -59,6 +60,36 @@ def lib():
             fn.argtypes = args
         _lib = handle
     return _lib
+
+
+# Optional per-call timing hook: when set, every C-ABI launch site records a pair of
+# timing events on the stream the kernels go to and hands them to the hook as
+# hook(name, start_event, end_event, shape_dict).  None (the default) costs one test.
+_launch_hook: Optional[Callable] = None
+
+
+def set_launch_hook(hook: Optional[Callable]) -> None:
+    global _launch_hook
+    _launch_hook = hook
+
+
+@contextlib.contextmanager
+def launch_region(name: str, device: torch.device, **shape):
+    """Bracket the launches of one C-ABI call with timing events (when hooked).
+
+    The events go on the device's current torch stream, which is the stream every
+    entry point is given (stream_of)."""
+    hook = _launch_hook
+    if hook is None:
+        yield
+        return
+    s = torch.cuda.current_stream(device)
+    e0 = torch.cuda.Event(enable_timing=True)
+    e1 = torch.cuda.Event(enable_timing=True)
+    e0.record(s)
+    yield
+    e1.record(s)
+    hook(name, e0, e1, shape)
 
 
 def exported_symbols():

@@ -66,9 +66,10 @@ def mu_qkv_project(x: torch.Tensor, mu: Optional[torch.Tensor], w_pack: torch.Te
     if w_pack.stride(-1) != 1:
         raise ValueError("mu_qkv_project: packed weight must be unit-stride in K")
     out = torch.empty(*lead, N, dtype=x.dtype, device=x.device)
-    nat.check(nat.lib().cdx_mu_qkv_fwd(x2.data_ptr(), ldx, nat.ptr(mu2), ldmu, w_pack.data_ptr(),
-                                       w_pack.stride(0), M, H, N, out.data_ptr(), N,
-                                       nat.stream_of(x)), "cdx_mu_qkv_fwd")
+    with nat.launch_region("mu_qkv", x.device, M=M, H=H, N=N, mu=mu2 is not None):
+        nat.check(nat.lib().cdx_mu_qkv_fwd(x2.data_ptr(), ldx, nat.ptr(mu2), ldmu, w_pack.data_ptr(),
+                                           w_pack.stride(0), M, H, N, out.data_ptr(), N,
+                                           nat.stream_of(x)), "cdx_mu_qkv_fwd")
     return out
 
 

@@ -60,9 +60,11 @@ def add_rms_norm(x: torch.Tensor, residual: Optional[torch.Tensor], weight: torc
     h = None
     if residual is not None and store_residual:
         h = residual_out if residual_out is not None else torch.empty(shape, dtype=x.dtype, device=x.device)
-    nat.check(nat.lib().cdx_add_rmsnorm_fwd(
-        x2.data_ptr(), nat.ptr(r2), w.data_ptr(), float(eps), x2.shape[0], H,
-        y.data_ptr(), nat.ptr(h), nat.stream_of(x)), "cdx_add_rmsnorm_fwd")
+    with nat.launch_region("add_rmsnorm" if r2 is not None else "rmsnorm", x.device, T=x2.shape[0], H=H,
+                           residual=r2 is not None, store_residual=h is not None):
+        nat.check(nat.lib().cdx_add_rmsnorm_fwd(
+            x2.data_ptr(), nat.ptr(r2), w.data_ptr(), float(eps), x2.shape[0], H,
+            y.data_ptr(), nat.ptr(h), nat.stream_of(x)), "cdx_add_rmsnorm_fwd")
     return y, h
 
 

@@ -74,10 +74,11 @@ def route_plan(ids: torch.Tensor, token_map: Optional[torch.Tensor], num_experts
     lib = nat.lib()
     ws_bytes = lib.cdx_route_workspace_bytes(T, num_experts)
     ws = torch.empty(max(ws_bytes, 16), dtype=torch.uint8, device=dev)
-    nat.check(lib.cdx_route_plan(ids.data_ptr(), T, nat.ptr(token_map), V, num_experts,
-                                 expert_id.data_ptr(), perm.data_ptr(), inv_perm.data_ptr(),
-                                 counts.data_ptr(), offsets.data_ptr(), ws.data_ptr(), ws_bytes,
-                                 nat.stream_of(ids)), "cdx_route_plan")
+    with nat.launch_region("route_plan", dev, T=T, E=num_experts, V=V):
+        nat.check(lib.cdx_route_plan(ids.data_ptr(), T, nat.ptr(token_map), V, num_experts,
+                                     expert_id.data_ptr(), perm.data_ptr(), inv_perm.data_ptr(),
+                                     counts.data_ptr(), offsets.data_ptr(), ws.data_ptr(), ws_bytes,
+                                     nat.stream_of(ids)), "cdx_route_plan")
     return RoutePlan(expert_id, perm, inv_perm, counts, offsets, num_experts)
 
 
@@ -194,10 +195,11 @@ def moe_swiglu(x2d: torch.Tensor, plan: RoutePlan, w_gu: torch.Tensor, w_down: t
         raise ValueError("moe_swiglu: packed weight shapes do not match the plan/hidden size")
     out = torch.empty_like(x2d)
     inter = torch.empty(T, S * P, dtype=x2d.dtype, device=x2d.device)
-    nat.check(nat.lib().cdx_moe_swiglu_fwd(x2d.data_ptr(), T, H, ie, E, int(has_shared),
-                                           plan.perm.data_ptr(), plan.offsets.data_ptr(),
-                                           w_gu.data_ptr(), w_down.data_ptr(), inter.data_ptr(),
-                                           out.data_ptr(), nat.stream_of(x2d)), "cdx_moe_swiglu_fwd")
+    with nat.launch_region("moe_swiglu", x2d.device, T=T, H=H, Ie=ie, E=E, shared=has_shared):
+        nat.check(nat.lib().cdx_moe_swiglu_fwd(x2d.data_ptr(), T, H, ie, E, int(has_shared),
+                                               plan.perm.data_ptr(), plan.offsets.data_ptr(),
+                                               w_gu.data_ptr(), w_down.data_ptr(), inter.data_ptr(),
+                                               out.data_ptr(), nat.stream_of(x2d)), "cdx_moe_swiglu_fwd")
     return out
 
 
