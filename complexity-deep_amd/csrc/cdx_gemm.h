@@ -3,19 +3,27 @@
 // C[m, n] = sum_k A[m, k] * B[n, k]: both operands K-contiguous ("NT"), which is the
 // natural layout of nn.Linear weights ([out, in]) and of packed expert weights.
 //
-// Block tile BM x BN x 64, 256 threads = 2 x 2 waves, each wave owning a
-// (BM/2) x (BN/2) sub-tile made of 32x32 blocks computed with
-// v_mfma_f32_32x32x16_bf16 (fp32 accumulators).
+// Block tile 256 x 256 x 64, 256 threads = 2 x 2 waves (one wave per SIMD), each wave
+// owning a 128 x 128 sub-tile made of 4 x 4 blocks of 32 x 32 computed with
+// v_mfma_f32_32x32x16_bf16 (256 fp32 accumulators per lane, held in AGPRs).
 //
-// Data movement per K-step of 64:
-//   global -> registers: every thread loads 16-byte chunks (8 bf16 along K); eight
-//     consecutive threads cover one 128-byte row segment, so a wave reads eight full
-//     rows per instruction.
-//   registers -> LDS: rows of 128 bytes, 16-byte chunk c of row r stored at chunk
-//     c ^ (r & 7).  The MFMA fragment reads (32 rows x one chunk per half-wave) then
-//     touch eight different chunk positions per eight lanes: no bank conflicts.
-//   LDS is double buffered; the global loads of step k+1 are in flight while the
-//   MFMAs of step k run, and one barrier per step separates the phases.
+// Global -> LDS: direct-to-LDS loads (global_load_lds_dwordx4).  One wave instruction
+// writes 64 x 16 bytes = 1 KB of LDS contiguously (lane i at base + 16 i), i.e. eight
+// 128-byte tile rows.  The LDS tile is row-major, 128 bytes per row (64 bf16 of K),
+// with 16-byte chunk c of row r stored at chunk position c ^ (r & 7); the swizzle is
+// applied on the load side: lane i of a block fetches global chunk (i & 7) ^ (i >> 3)
+// of row (i >> 3).  Fragment reads (32 rows x one chunk per half wave) then touch
+// eight distinct chunk positions per eight lanes: no LDS bank conflicts.
+//
+// Pipeline (two LDS stages of 64 KB each; four K16 sub-steps per 64-wide K step):
+//   sub-steps 0..2:  read the fragments of sub-step s+1 into the spare register set,
+//                    then issue the 16 MFMAs of sub-step s.
+//   sub-step 3:      wait for this wave's DMA of step k+1 (vmcnt(0)), barrier (now
+//                    every wave's DMA landed and every wave finished reading stage
+//                    k), issue the DMA of step k+2 into stage k, read sub-step 0 of
+//                    step k+1, then issue the MFMAs of sub-step 3.
+// One barrier per K step; its latency is covered by the MFMAs of sub-step 3, whose
+// operands are already in registers.  The DMA of a step has a whole K step to land.
 //
 // Operand order: the MFMA is issued as mfma(B_frag, A_frag), producing D = C^T for
 // the 32x32 block.  In the gfx950 32x32 output layout lane l holds column l%32 and
@@ -61,6 +69,10 @@ struct GemmParams {
   int32_t nt_count;
 };
 
+constexpr int kBM = 256;
+constexpr int kBN = 256;
+constexpr int kBK = 64;
+constexpr int kGemmThreads = 256;
 constexpr int kGroupM = 4;
 constexpr int kNumXcd = 8;
 
@@ -72,19 +84,29 @@ __device__ __forceinline__ int xcd_remap(int b, int nb) {
 
 __device__ __forceinline__ float silu_f32(float g) { return g / (1.0f + __expf(-g)); }
 
-template <int BM, int BN, ALoad AL, Epi EP>
-__global__ __launch_bounds__(256, 1) void gemm_nt_kernel(const GemmParams p) {
-  constexpr int BK = 64;
-  constexpr int ROW_BYTES = BK * 2;       // 128 bytes per tile row
-  constexpr int WM = BM / 2, WN = BN / 2;
-  constexpr int MI = WM / 32, NI = WN / 32;
-  constexpr int A_LD = BM * BK / 8 / 256;  // 16-byte chunks per thread per step
-  constexpr int B_LD = BN * BK / 8 / 256;
-  constexpr int A_BYTES = BM * ROW_BYTES, B_BYTES = BN * ROW_BYTES;
-  static_assert(MI >= 1 && NI >= 1 && A_LD >= 1 && B_LD >= 1, "tile too small");
+// s_waitcnt immediate (gfx9 layout: vmcnt bits 3:0 and 15:14, expcnt 6:4, lgkmcnt 11:8).
+constexpr int waitcnt_imm(int vm, int lgkm) {
+  return (vm & 15) | ((vm >> 4) << 14) | (7 << 4) | ((lgkm & 15) << 8);
+}
+
+// 16 bytes from global memory straight into LDS at lds_block + 16 * lane.
+__device__ __forceinline__ void dma16(const uint16_t* g, uint8_t* lds_block) {
+  __builtin_amdgcn_global_load_lds((const __attribute__((address_space(1))) void*)g,
+                                   (__attribute__((address_space(3))) void*)lds_block, 16, 0, 0);
+}
+
+template <ALoad AL, Epi EP>
+__global__ __launch_bounds__(kGemmThreads, 1) void gemm_nt_kernel(const GemmParams p) {
+  constexpr int ROW_BYTES = kBK * 2;                // 128 bytes per tile row
+  constexpr int TILE_BYTES = kBM * ROW_BYTES;       // 32 KB per operand and stage
+  constexpr int STAGE_BYTES = 2 * TILE_BYTES;
+  constexpr int WM = kBM / 2, WN = kBN / 2;
+  constexpr int MI = WM / 32, NI = WN / 32;         // 4 x 4 blocks of 32 x 32
+  constexpr int LD_PER_WAVE = kBM / 8 / 4;          // 1 KB DMA blocks per wave and operand: 8
+  static_assert(kBM == kBN, "A and B tiles share the DMA layout");
   static_assert(EP != Epi::kSwiGLU || (WN % 64) == 0, "SwiGLU needs gate/up pairs per wave");
 
-  __shared__ __attribute__((aligned(16))) uint8_t lds[2 * (A_BYTES + B_BYTES)];
+  __shared__ __attribute__((aligned(1024))) uint8_t lds[2 * STAGE_BYTES];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -108,10 +130,10 @@ __global__ __launch_bounds__(256, 1) void gemm_nt_kernel(const GemmParams p) {
     e = -1;
     for (int x = 0; x < p.E; ++x) {
       const int s0 = p.offsets[x], s1 = p.offsets[x + 1];
-      const int ntile = (s1 - s0 + BM - 1) / BM;
+      const int ntile = (s1 - s0 + kBM - 1) / kBM;
       if (mt < before + ntile) {
         e = x;
-        m0 = s0 + (int64_t)(mt - before) * BM;
+        m0 = s0 + (int64_t)(mt - before) * kBM;
         m_end = s1;
         break;
       }
@@ -119,59 +141,71 @@ __global__ __launch_bounds__(256, 1) void gemm_nt_kernel(const GemmParams p) {
     }
     if (e < 0) return;
   } else {
-    m0 = (int64_t)mt * BM;
+    m0 = (int64_t)mt * kBM;
     m_end = p.M;
     if (m0 >= m_end) return;
   }
-  const int n0 = nt * BN;
+  const int n0 = nt * kBN;
 
-  // ---- per-thread global source rows ----------------------------------------
-  const int ld_row = tid >> 3;  // 0..31
-  const int ld_chunk = tid & 7;
-  const uint16_t* a_src[A_LD];
-  const uint16_t* a2_src[A_LD];
+  // ---- per-lane DMA sources ------------------------------------------------
+  // Wave w fills tile rows [64 w, 64 w + 64) of both operands, eight rows per
+  // instruction; lane i of instruction j covers row 64 w + 8 j + (i >> 3) and
+  // fetches its swizzled chunk.
+  const int dr = lane >> 3;
+  const int dchunk = (lane & 7) ^ dr;
+  const uint16_t* a_src[LD_PER_WAVE];
+  const uint16_t* a2_src[LD_PER_WAVE];
+  const uint16_t* b_src[LD_PER_WAVE];
+  const uint16_t* bexp = p.b + (int64_t)e * p.b_estride;
 #pragma unroll
-  for (int i = 0; i < A_LD; ++i) {
-    int64_t gm = m0 + ld_row + i * 32;
+  for (int j = 0; j < LD_PER_WAVE; ++j) {
+    const int r = wave * 64 + j * 8 + dr;
+    int64_t gm = m0 + r;
     gm = gm < m_end ? gm : m_end - 1;  // rows past the segment are loaded but never stored
     const int64_t row = (AL == ALoad::kGather) ? (int64_t)p.perm[gm] : gm;
-    a_src[i] = p.a + row * p.lda + ld_chunk * 8;
-    if (AL == ALoad::kConcat) a2_src[i] = p.a2 + row * p.lda2 + ld_chunk * 8;
-  }
-  const uint16_t* bexp = p.b + (int64_t)e * p.b_estride;
-  const uint16_t* b_src[B_LD];
-#pragma unroll
-  for (int i = 0; i < B_LD; ++i) {
-    int n = n0 + ld_row + i * 32;
+    a_src[j] = p.a + row * p.lda + dchunk * 8;
+    if (AL == ALoad::kConcat) a2_src[j] = p.a2 + row * p.lda2 + dchunk * 8;
+    int n = n0 + r;
     n = n < p.N ? n : p.N - 1;
-    b_src[i] = bexp + (int64_t)n * p.ldb + ld_chunk * 8;
+    b_src[j] = bexp + (int64_t)n * p.ldb + dchunk * 8;
   }
-  // LDS destination of this thread's chunks: row ld_row + 32 i, swizzled chunk.
-  const int st_off = ld_row * ROW_BYTES + ((ld_chunk ^ (ld_row & 7)) << 4);
+  const int dma_off = wave * 64 * ROW_BYTES;  // this wave's first 1 KB block in a tile
 
-  uint4 ra[A_LD], rb[B_LD];
-  auto gload = [&](int kt) {
-    const int k0 = kt * BK;
+  auto issue = [&](int kt, int stage) __attribute__((always_inline)) {
+    const int k0 = kt * kBK;
+    uint8_t* As = lds + stage * STAGE_BYTES + dma_off;
+    uint8_t* Bs = As + TILE_BYTES;
 #pragma unroll
-    for (int i = 0; i < A_LD; ++i) {
+    for (int j = 0; j < LD_PER_WAVE; ++j) {
       const uint16_t* src;
       if (AL == ALoad::kConcat) {
-        src = (k0 < p.k_split) ? a_src[i] + k0 : a2_src[i] + (k0 - p.k_split);
+        src = (k0 < p.k_split) ? a_src[j] + k0 : a2_src[j] + (k0 - p.k_split);
       } else {
-        src = a_src[i] + k0;
+        src = a_src[j] + k0;
       }
-      ra[i] = *reinterpret_cast<const uint4*>(src);
+      dma16(src, As + j * 1024);
+      dma16(b_src[j] + k0, Bs + j * 1024);
     }
-#pragma unroll
-    for (int i = 0; i < B_LD; ++i) rb[i] = *reinterpret_cast<const uint4*>(b_src[i] + k0);
   };
-  auto sstore = [&](int buf) {
-    uint8_t* As = lds + buf * (A_BYTES + B_BYTES);
-    uint8_t* Bs = As + A_BYTES;
+
+  // ---- fragments -------------------------------------------------------------
+  // Row (lane & 31) of a 32-row block, chunk 2 s + (lane >> 5) for sub-step s.
+  const int fr_row = lane & 31;
+  int fr_off[4];
 #pragma unroll
-    for (int i = 0; i < A_LD; ++i) *reinterpret_cast<uint4*>(As + st_off + i * 32 * ROW_BYTES) = ra[i];
+  for (int s = 0; s < 4; ++s) fr_off[s] = fr_row * ROW_BYTES + (((2 * s + (lane >> 5)) ^ (fr_row & 7)) << 4);
+  const int a_frag_base = wm * WM * ROW_BYTES;
+  const int b_frag_base = TILE_BYTES + wn * WN * ROW_BYTES;
+
+  bf16x8 fa[2][MI], fb[2][NI];
+  auto read_frags = [&](int stage, int s, int set) __attribute__((always_inline)) {
+    const uint8_t* base = lds + stage * STAGE_BYTES;
 #pragma unroll
-    for (int i = 0; i < B_LD; ++i) *reinterpret_cast<uint4*>(Bs + st_off + i * 32 * ROW_BYTES) = rb[i];
+    for (int mi = 0; mi < MI; ++mi)
+      fa[set][mi] = *reinterpret_cast<const bf16x8*>(base + a_frag_base + mi * 32 * ROW_BYTES + fr_off[s]);
+#pragma unroll
+    for (int ni = 0; ni < NI; ++ni)
+      fb[set][ni] = *reinterpret_cast<const bf16x8*>(base + b_frag_base + ni * 32 * ROW_BYTES + fr_off[s]);
   };
 
   f32x16 acc[MI][NI];
@@ -182,39 +216,74 @@ __global__ __launch_bounds__(256, 1) void gemm_nt_kernel(const GemmParams p) {
 #pragma unroll
       for (int v = 0; v < 16; ++v) acc[mi][ni][v] = 0.f;
 
-  // Fragment read offsets: row (lane & 31) of a 32-row block, chunk 2 s + (lane >> 5).
-  const int fr_row = lane & 31;
-  int fr_off[4];
+  auto mfmas = [&](int set) __attribute__((always_inline)) {
 #pragma unroll
-  for (int s = 0; s < 4; ++s) fr_off[s] = fr_row * ROW_BYTES + (((2 * s + (lane >> 5)) ^ (fr_row & 7)) << 4);
-
-  const int KT = p.K / BK;
-  gload(0);
-  sstore(0);
-  __syncthreads();
-  for (int kt = 0; kt < KT; ++kt) {
-    const int cur = kt & 1;
-    if (kt + 1 < KT) gload(kt + 1);
-    const uint8_t* As = lds + cur * (A_BYTES + B_BYTES) + wm * WM * ROW_BYTES;
-    const uint8_t* Bs = lds + cur * (A_BYTES + B_BYTES) + A_BYTES + wn * WN * ROW_BYTES;
-#pragma unroll
-    for (int s = 0; s < 4; ++s) {
-      bf16x8 af[MI], bfg[NI];
-#pragma unroll
-      for (int mi = 0; mi < MI; ++mi)
-        af[mi] = *reinterpret_cast<const bf16x8*>(As + mi * 32 * ROW_BYTES + fr_off[s]);
+    for (int mi = 0; mi < MI; ++mi)
 #pragma unroll
       for (int ni = 0; ni < NI; ++ni)
-        bfg[ni] = *reinterpret_cast<const bf16x8*>(Bs + ni * 32 * ROW_BYTES + fr_off[s]);
+        acc[mi][ni] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fb[set][ni], fa[set][mi], acc[mi][ni], 0, 0, 0);
+  };
+
+  // ---- main loop --------------------------------------------------------------
+  // Scheduling masks of __builtin_amdgcn_sched_group_barrier.
+  constexpr int kSchedMfma = 0x008, kSchedVmem = 0x010, kSchedDsRead = 0x100;
+
+  // Sub-steps 0..2 of a K step: MFMAs of sub-step s from register set s & 1, with
+  // the eight fragment reads of sub-step s+1 slotted behind the first eight MFMAs,
+  // so they have landed long before the next sub-step needs them.
+  auto substep = [&](int stage, int s) __attribute__((always_inline)) {
+    read_frags(stage, s + 1, (s + 1) & 1);
+    mfmas(s & 1);
 #pragma unroll
-      for (int mi = 0; mi < MI; ++mi)
-#pragma unroll
-        for (int ni = 0; ni < NI; ++ni)
-          acc[mi][ni] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(bfg[ni], af[mi], acc[mi][ni], 0, 0, 0);
+    for (int i = 0; i < 8; ++i) {
+      __builtin_amdgcn_sched_group_barrier(kSchedMfma, 1, 0);
+      __builtin_amdgcn_sched_group_barrier(kSchedDsRead, 1, 0);
     }
-    if (kt + 1 < KT) sstore(cur ^ 1);
+    __builtin_amdgcn_sched_group_barrier(kSchedMfma, 8, 0);
+    __builtin_amdgcn_sched_barrier(0);
+  };
+  // Sub-step 3: barrier, then its MFMAs (set 1) interleaved with the DMA of step
+  // kt+2 into this stage and the reads of sub-step 0 of step kt+1 from the other.
+  auto last_substep = [&](int kt, int stage, bool dma, bool next) __attribute__((always_inline)) {
+    __builtin_amdgcn_s_waitcnt(waitcnt_imm(0, 0));  // own DMA of kt+1 landed, own reads done
     __syncthreads();
+    if (dma) issue(kt + 2, stage);
+    if (next) read_frags(stage ^ 1, 0, 0);
+    mfmas(1);
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      __builtin_amdgcn_sched_group_barrier(kSchedMfma, 1, 0);
+      __builtin_amdgcn_sched_group_barrier(kSchedVmem, 1, 0);
+      if (i < 8) __builtin_amdgcn_sched_group_barrier(kSchedDsRead, 1, 0);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+  };
+  auto kstep = [&](int kt, bool dma, bool next) __attribute__((always_inline)) {
+    const int stage = kt & 1;
+    substep(stage, 0);
+    substep(stage, 1);
+    substep(stage, 2);
+    last_substep(kt, stage, dma, next);
+  };
+
+  const int KT = p.K / kBK;
+  issue(0, 0);
+  if (KT > 1) {
+    issue(1, 1);
+    // step 0's 2 * LD_PER_WAVE loads of this wave landed (step 1's may be in flight)
+    __builtin_amdgcn_s_waitcnt(waitcnt_imm(2 * LD_PER_WAVE, 15));
+  } else {
+    __builtin_amdgcn_s_waitcnt(waitcnt_imm(0, 15));
   }
+  __syncthreads();
+  read_frags(0, 0, 0);
+  __builtin_amdgcn_s_waitcnt(waitcnt_imm(63, 0));
+  __builtin_amdgcn_sched_barrier(0);
+
+  int kt = 0;
+  for (; kt + 2 < KT; ++kt) kstep(kt, true, true);
+  if (kt + 1 < KT) kstep(kt++, false, true);
+  kstep(kt, false, false);
 
   // ---- epilogue --------------------------------------------------------------
   const int hi = lane >> 5;

@@ -8,13 +8,13 @@
 namespace cdx {
 namespace {
 
-template <int BM, int BN, ALoad AL, Epi EP>
+template <ALoad AL, Epi EP>
 int launch(GemmParams p, hipStream_t s, const char* name) {
-  p.nt_count = (p.N + BN - 1) / BN;
+  p.nt_count = (p.N + kBN - 1) / kBN;
   const int64_t nb = (int64_t)p.mt_count * p.nt_count;
   if (nb == 0) return CDX_OK;
   if (nb > INT32_MAX) return fail(CDX_EUNSUPPORTED, "%s: problem too large (%lld tiles)", name, (long long)nb);
-  gemm_nt_kernel<BM, BN, AL, EP><<<dim3((unsigned)nb), dim3(256), 0, s>>>(p);
+  gemm_nt_kernel<AL, EP><<<dim3((unsigned)nb), dim3(kGemmThreads), 0, s>>>(p);
   return check_launch(name);
 }
 
@@ -62,12 +62,11 @@ extern "C" int cdx_mu_qkv_fwd(const uint16_t* x, int64_t ldx, const uint16_t* mu
   p.K = (int32_t)K;
   p.c = out;
   p.ldc = ldo;
-  constexpr int BM = 256, BN = 256;
-  if (cdiv(M, BM) > INT32_MAX) return fail(CDX_EUNSUPPORTED, "%s: M too large", name);
-  p.mt_count = (int32_t)cdiv(M, BM);
+  if (cdiv(M, kBM) > INT32_MAX) return fail(CDX_EUNSUPPORTED, "%s: M too large", name);
+  p.mt_count = (int32_t)cdiv(M, kBM);
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
-  if (mu) return launch<BM, BN, ALoad::kConcat, Epi::kStore>(p, s, name);
-  return launch<BM, BN, ALoad::kDense, Epi::kStore>(p, s, name);
+  if (mu) return launch<ALoad::kConcat, Epi::kStore>(p, s, name);
+  return launch<ALoad::kDense, Epi::kStore>(p, s, name);
 }
 
 extern "C" int cdx_moe_swiglu_fwd(const uint16_t* x, int64_t T, int32_t H, int32_t Ie, int32_t E,
@@ -90,8 +89,7 @@ extern "C" int cdx_moe_swiglu_fwd(const uint16_t* x, int64_t T, int32_t H, int32
   const int32_t n_gu = 2 * S * P;
   const int32_t k_down = S * P;
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
-  constexpr int BM = 256, BN = 256;
-  const int32_t mt = (int32_t)(cdiv(T, BM) + E);
+  const int32_t mt = (int32_t)(cdiv(T, kBM) + E);
 
   // Pass 1: gathered rows x[perm] times the expert's gate/up rows, SwiGLU epilogue.
   GemmParams p1{};
@@ -110,7 +108,7 @@ extern "C" int cdx_moe_swiglu_fwd(const uint16_t* x, int64_t T, int32_t H, int32
   p1.c = inter;
   p1.ldc = k_down;
   p1.mt_count = mt;
-  if (int rc = launch<BM, BN, ALoad::kGather, Epi::kSwiGLU>(p1, s, name)) return rc;
+  if (int rc = launch<ALoad::kGather, Epi::kSwiGLU>(p1, s, name)) return rc;
 
   // Pass 2: activations (sorted order) times [shared_down | down[e]], rows scattered back.
   GemmParams p2{};
@@ -129,7 +127,7 @@ extern "C" int cdx_moe_swiglu_fwd(const uint16_t* x, int64_t T, int32_t H, int32
   p2.c = out;
   p2.ldc = H;
   p2.mt_count = mt;
-  return launch<BM, BN, ALoad::kDense, Epi::kScatter>(p2, s, name);
+  return launch<ALoad::kDense, Epi::kScatter>(p2, s, name);
 }
 
 extern "C" int cdx_grouped_gemm_fwd(const uint16_t* a, int64_t T, int32_t K, int32_t N, int32_t E,
@@ -160,7 +158,6 @@ extern "C" int cdx_grouped_gemm_fwd(const uint16_t* a, int64_t T, int32_t K, int
   p.K = K;
   p.c = out;
   p.ldc = N;
-  constexpr int BM = 256, BN = 256;
-  p.mt_count = (int32_t)(cdiv(T, BM) + E);
-  return launch<BM, BN, ALoad::kDense, Epi::kStore>(p, reinterpret_cast<hipStream_t>(stream), name);
+  p.mt_count = (int32_t)(cdiv(T, kBM) + E);
+  return launch<ALoad::kDense, Epi::kStore>(p, reinterpret_cast<hipStream_t>(stream), name);
 }
