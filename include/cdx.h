@@ -109,7 +109,7 @@ int cdx_unpermute_rows(const void* in_dev, const int32_t* perm_dev, int64_t T,
 
 /*
  * Packed weight layouts (bf16, K-contiguous, built once by the caller):
- *   P   = round_up(Ie, 32)                  padded expert width
+ *   P   = round_up(Ie, 64)                  padded expert width
  *   S   = has_shared ? 2 : 1                number of SwiGLU blocks per token
  *   w_gu   [E][S*2*P][H]   gate/up rows for the shared block (if any) then the routed
  *                          block; inside a block, rows come in groups of 64:
