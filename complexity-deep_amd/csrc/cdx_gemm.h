@@ -3,7 +3,7 @@
 // C[m, n] = sum_k A[m, k] * B[n, k]: both operands K-contiguous ("NT"), which is the
 // natural layout of nn.Linear weights ([out, in]) and of packed expert weights.
 //
-// Block tile 256 x 256 x 64, 256 threads = 2 x 2 waves (one wave per SIMD), each wave
+// Block tile 256 x 256 (x kBK per LDS stage), 256 threads = 2 x 2 waves (one wave per SIMD), each wave
 // owning a 128 x 128 sub-tile made of 4 x 4 blocks of 32 x 32 computed with
 // v_mfma_f32_32x32x16_bf16 (256 fp32 accumulators per lane, held in AGPRs).
 //
@@ -70,11 +70,26 @@ struct GemmParams {
 };
 
 constexpr int kBM = 256;
-constexpr int kBN = 256;
-constexpr int kBK = 64;
 constexpr int kGemmThreads = 256;
 constexpr int kGroupM = 4;
 constexpr int kNumXcd = 8;
+
+// Tile configuration: BN output columns per block, BK-deep LDS stages, STAGES of
+// them in flight, MINB blocks resident per CU.  Stage s holds the A (256 x BK) and B
+// (BN x BK) tiles of one K step; the DMA of step k + STAGES is issued as soon as
+// stage k is consumed, so a load has STAGES - 1 K steps to land.
+template <int BN_, int BK_, int STAGES_, int MINB_>
+struct GemmCfg {
+  static constexpr int BN = BN_, BK = BK_, STAGES = STAGES_, MINB = MINB_;
+  static_assert(BN == 256 || BN == 128, "BN must be 128 or 256");
+  static_assert(BK == 32 || BK == 64, "BK must be 32 or 64");
+  static constexpr int STAGE_BYTES = (kBM + BN) * BK * 2;
+  static_assert(STAGES >= 2 && STAGES * STAGE_BYTES * MINB <= 160 * 1024, "stages must fit 160 KB of LDS");
+};
+#ifndef CDX_GEMM_CFG
+#define CDX_GEMM_CFG 256, 64, 2, 1
+#endif
+using DefaultCfg = GemmCfg<CDX_GEMM_CFG>;
 
 __device__ __forceinline__ int xcd_remap(int b, int nb) {
   const int q = nb / kNumXcd, r = nb % kNumXcd;
@@ -95,22 +110,32 @@ __device__ __forceinline__ void dma16(const uint16_t* g, uint8_t* lds_block) {
                                    (__attribute__((address_space(3))) void*)lds_block, 16, 0, 0);
 }
 
-template <ALoad AL, Epi EP>
-__global__ __launch_bounds__(kGemmThreads, 1) void gemm_nt_kernel(const GemmParams p) {
-  constexpr int ROW_BYTES = kBK * 2;                // 128 bytes per tile row
-  constexpr int TILE_BYTES = kBM * ROW_BYTES;       // 32 KB per operand and stage
-  constexpr int STAGE_BYTES = 2 * TILE_BYTES;
+template <class Cfg, ALoad AL, Epi EP>
+__global__ __launch_bounds__(kGemmThreads, Cfg::MINB) void gemm_nt_kernel(const GemmParams p) {
+  constexpr int kBN = Cfg::BN, kBK = Cfg::BK, kStages = Cfg::STAGES;
+  constexpr int ROW_BYTES = kBK * 2;                // bytes per tile row in LDS
+  constexpr int CPR = kBK / 8;                      // 16-byte chunks per row
+  constexpr int RPL = 256 / ROW_BYTES;              // rows per 256-byte bank line (64 banks)
+  constexpr int A_TILE_BYTES = kBM * ROW_BYTES;     // one stage of A
+  constexpr int STAGE_BYTES = Cfg::STAGE_BYTES;     // A then B
   constexpr int WM = kBM / 2, WN = kBN / 2;
-  constexpr int MI = WM / 32, NI = WN / 32;         // 4 x 4 blocks of 32 x 32
-  constexpr int LD_PER_WAVE = kBM / 8 / 4;          // 1 KB DMA blocks per wave and operand: 8
-  static_assert(kBM == kBN, "A and B tiles share the DMA layout");
+  constexpr int MI = WM / 32, NI = WN / 32;         // blocks of 32 x 32 per wave
+  constexpr int ROWS_PER_DMA = 1024 / ROW_BYTES;    // rows one wave instruction fills
+  constexpr int LD_A = kBM / ROWS_PER_DMA / 4;      // DMA instructions per wave and K step, A
+  constexpr int LD_B = kBN / ROWS_PER_DMA / 4;      // and B
+  constexpr int LD_PER_STEP = LD_A + LD_B;
+  constexpr int NSUB = kBK / 16;                    // K16 sub-steps per K step
+  constexpr int NFRAG = MI + NI;                    // fragment reads per sub-step
+  static_assert(LD_B >= 1, "B tile too small for the DMA layout");
   static_assert(EP != Epi::kSwiGLU || (WN % 64) == 0, "SwiGLU needs gate/up pairs per wave");
+  static_assert(LD_PER_STEP * (kStages - 1) <= 63, "vmcnt range");
 
-  __shared__ __attribute__((aligned(1024))) uint8_t lds[2 * STAGE_BYTES];
+  __shared__ __attribute__((aligned(1024))) uint8_t lds[kStages * STAGE_BYTES];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
-  const int wave = tid >> 6;
+  // Wave-uniform, so LDS addresses (the DMA's M0 in particular) stay scalar.
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int wm = wave >> 1, wn = wave & 1;
 
   // ---- tile decode -------------------------------------------------------
@@ -148,64 +173,82 @@ __global__ __launch_bounds__(kGemmThreads, 1) void gemm_nt_kernel(const GemmPara
   const int n0 = nt * kBN;
 
   // ---- per-lane DMA sources ------------------------------------------------
-  // Wave w fills tile rows [64 w, 64 w + 64) of both operands, eight rows per
-  // instruction; lane i of instruction j covers row 64 w + 8 j + (i >> 3) and
-  // fetches its swizzled chunk.
-  const int dr = lane >> 3;
-  const int dchunk = (lane & 7) ^ dr;
-  const uint16_t* a_src[LD_PER_WAVE];
-  const uint16_t* a2_src[LD_PER_WAVE];
-  const uint16_t* b_src[LD_PER_WAVE];
+  // LDS rows are ROW_BYTES long; 16-byte chunk c of tile row r sits at chunk
+  // position c ^ ((r / RPL) % CPR).  The LDS serves a 128-bit read 16 lanes at a
+  // time from 64 banks (256 bytes); the 16 rows one fragment read touches per 16
+  // lanes then cover every bank exactly once.  The swizzle is applied on the load
+  // side: lane i of a DMA instruction fills position i % CPR of row i / CPR of its
+  // 1 KB block and therefore fetches global chunk (i % CPR) ^ ((row / RPL) % CPR).
+  // Wave w fills rows [64 w, 64 w + 64) of both operands.
+  const int dr = lane / CPR;
+  const uint16_t* a_src[LD_A];
+  const uint16_t* a2_src[LD_A];
+  const uint16_t* b_src[LD_B];
   const uint16_t* bexp = p.b + (int64_t)e * p.b_estride;
 #pragma unroll
-  for (int j = 0; j < LD_PER_WAVE; ++j) {
-    const int r = wave * 64 + j * 8 + dr;
+  for (int j = 0; j < LD_A; ++j) {
+    const int r = wave * (kBM / 4) + j * ROWS_PER_DMA + dr;
+    const int dchunk = (lane % CPR) ^ ((r / RPL) % CPR);
     int64_t gm = m0 + r;
     gm = gm < m_end ? gm : m_end - 1;  // rows past the segment are loaded but never stored
     const int64_t row = (AL == ALoad::kGather) ? (int64_t)p.perm[gm] : gm;
     a_src[j] = p.a + row * p.lda + dchunk * 8;
     if (AL == ALoad::kConcat) a2_src[j] = p.a2 + row * p.lda2 + dchunk * 8;
+  }
+#pragma unroll
+  for (int j = 0; j < LD_B; ++j) {
+    const int r = wave * (kBN / 4) + j * ROWS_PER_DMA + dr;
+    const int dchunk = (lane % CPR) ^ ((r / RPL) % CPR);
     int n = n0 + r;
     n = n < p.N ? n : p.N - 1;
     b_src[j] = bexp + (int64_t)n * p.ldb + dchunk * 8;
   }
-  const int dma_off = wave * 64 * ROW_BYTES;  // this wave's first 1 KB block in a tile
+  const int a_dma_off = wave * (kBM / 4) * ROW_BYTES;  // this wave's first DMA block in A
+  const int b_dma_off = A_TILE_BYTES + wave * (kBN / 4) * ROW_BYTES;
 
-  auto issue = [&](int kt, int stage) __attribute__((always_inline)) {
+  // One DMA instruction of step kt into `stage`: d < LD_A covers A rows, then B.
+  auto dma1 = [&](int kt, int stage, int d) __attribute__((always_inline)) {
     const int k0 = kt * kBK;
-    uint8_t* As = lds + stage * STAGE_BYTES + dma_off;
-    uint8_t* Bs = As + TILE_BYTES;
-#pragma unroll
-    for (int j = 0; j < LD_PER_WAVE; ++j) {
+    if (d < LD_A) {
       const uint16_t* src;
       if (AL == ALoad::kConcat) {
-        src = (k0 < p.k_split) ? a_src[j] + k0 : a2_src[j] + (k0 - p.k_split);
+        src = (k0 < p.k_split) ? a_src[d] + k0 : a2_src[d] + (k0 - p.k_split);
       } else {
-        src = a_src[j] + k0;
+        src = a_src[d] + k0;
       }
-      dma16(src, As + j * 1024);
-      dma16(b_src[j] + k0, Bs + j * 1024);
+      dma16(src, lds + stage * STAGE_BYTES + a_dma_off + d * 1024);
+    } else {
+      dma16(b_src[d - LD_A] + k0, lds + stage * STAGE_BYTES + b_dma_off + (d - LD_A) * 1024);
     }
+  };
+  auto issue = [&](int kt, int stage) __attribute__((always_inline)) {
+#pragma unroll
+    for (int d = 0; d < LD_PER_STEP; ++d) dma1(kt, stage, d);
   };
 
   // ---- fragments -------------------------------------------------------------
   // Row (lane & 31) of a 32-row block, chunk 2 s + (lane >> 5) for sub-step s.
   const int fr_row = lane & 31;
-  int fr_off[4];
+  int fr_off[NSUB];
 #pragma unroll
-  for (int s = 0; s < 4; ++s) fr_off[s] = fr_row * ROW_BYTES + (((2 * s + (lane >> 5)) ^ (fr_row & 7)) << 4);
+  for (int s = 0; s < NSUB; ++s)
+    fr_off[s] = fr_row * ROW_BYTES + (((2 * s + (lane >> 5)) ^ ((fr_row / RPL) % CPR)) << 4);
   const int a_frag_base = wm * WM * ROW_BYTES;
-  const int b_frag_base = TILE_BYTES + wn * WN * ROW_BYTES;
+  const int b_frag_base = A_TILE_BYTES + wn * WN * ROW_BYTES;
 
   bf16x8 fa[2][MI], fb[2][NI];
-  auto read_frags = [&](int stage, int s, int set) __attribute__((always_inline)) {
+  // Fragment f of sub-step s into register set `set`: f < MI is A block f, then B.
+  auto read1 = [&](int stage, int s, int set, int f) __attribute__((always_inline)) {
     const uint8_t* base = lds + stage * STAGE_BYTES;
+    if (f < MI) {
+      fa[set][f] = *reinterpret_cast<const bf16x8*>(base + a_frag_base + f * 32 * ROW_BYTES + fr_off[s]);
+    } else {
+      fb[set][f - MI] = *reinterpret_cast<const bf16x8*>(base + b_frag_base + (f - MI) * 32 * ROW_BYTES + fr_off[s]);
+    }
+  };
+  auto read_frags = [&](int stage, int s, int set) __attribute__((always_inline)) {
 #pragma unroll
-    for (int mi = 0; mi < MI; ++mi)
-      fa[set][mi] = *reinterpret_cast<const bf16x8*>(base + a_frag_base + mi * 32 * ROW_BYTES + fr_off[s]);
-#pragma unroll
-    for (int ni = 0; ni < NI; ++ni)
-      fb[set][ni] = *reinterpret_cast<const bf16x8*>(base + b_frag_base + ni * 32 * ROW_BYTES + fr_off[s]);
+    for (int f = 0; f < NFRAG; ++f) read1(stage, s, set, f);
   };
 
   f32x16 acc[MI][NI];
@@ -216,62 +259,66 @@ __global__ __launch_bounds__(kGemmThreads, 1) void gemm_nt_kernel(const GemmPara
 #pragma unroll
       for (int v = 0; v < 16; ++v) acc[mi][ni][v] = 0.f;
 
-  auto mfmas = [&](int set) __attribute__((always_inline)) {
-#pragma unroll
-    for (int mi = 0; mi < MI; ++mi)
-#pragma unroll
-      for (int ni = 0; ni < NI; ++ni)
-        acc[mi][ni] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fb[set][ni], fa[set][mi], acc[mi][ni], 0, 0, 0);
+  auto mfma1 = [&](int set, int i) __attribute__((always_inline)) {
+    const int mi = i / NI, ni = i % NI;
+    acc[mi][ni] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fb[set][ni], fa[set][mi], acc[mi][ni], 0, 0, 0);
   };
 
   // ---- main loop --------------------------------------------------------------
-  // Scheduling masks of __builtin_amdgcn_sched_group_barrier.
-  constexpr int kSchedMfma = 0x008, kSchedVmem = 0x010, kSchedDsRead = 0x100;
-
-  // Sub-steps 0..2 of a K step: MFMAs of sub-step s from register set s & 1, with
-  // the eight fragment reads of sub-step s+1 slotted behind the first eight MFMAs,
-  // so they have landed long before the next sub-step needs them.
+  // The order of MFMAs, fragment reads and DMA instructions inside a sub-step is
+  // fixed by hand: each MFMA is followed by at most one read and one DMA, and a
+  // scheduling fence closes the group, so the memory instructions issue in the
+  // shadow of the MFMAs instead of in bursts.
+  //
+  // Sub-steps 0..NSUB-2 of a K step: MFMAs of sub-step s from register set s & 1,
+  // the NFRAG fragment reads of sub-step s+1 slotted behind the first MFMAs.
   auto substep = [&](int stage, int s) __attribute__((always_inline)) {
-    read_frags(stage, s + 1, (s + 1) & 1);
-    mfmas(s & 1);
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      __builtin_amdgcn_sched_group_barrier(kSchedMfma, 1, 0);
-      __builtin_amdgcn_sched_group_barrier(kSchedDsRead, 1, 0);
+    for (int i = 0; i < MI * NI; ++i) {
+      mfma1(s & 1, i);
+      if (i < NFRAG) read1(stage, s + 1, (s + 1) & 1, i);
+      __builtin_amdgcn_sched_barrier(0);
     }
-    __builtin_amdgcn_sched_group_barrier(kSchedMfma, 8, 0);
-    __builtin_amdgcn_sched_barrier(0);
   };
-  // Sub-step 3: barrier, then its MFMAs (set 1) interleaved with the DMA of step
-  // kt+2 into this stage and the reads of sub-step 0 of step kt+1 from the other.
-  auto last_substep = [&](int kt, int stage, bool dma, bool next) __attribute__((always_inline)) {
-    __builtin_amdgcn_s_waitcnt(waitcnt_imm(0, 0));  // own DMA of kt+1 landed, own reads done
+  // Last sub-step: wait until step kt+1 has landed (the DMA of later steps may stay
+  // in flight) and every wave is done with `stage`; then its MFMAs, each followed by
+  // one DMA instruction of step kt + kStages into the freed stage and one fragment
+  // read of sub-step 0 of step kt+1.
+  auto last_substep = [&](int kt, int stage, int next_stage, bool dma, bool next,
+                          bool drain) __attribute__((always_inline)) {
+    if (drain) {
+      __builtin_amdgcn_s_waitcnt(waitcnt_imm(0, 0));
+    } else {
+      __builtin_amdgcn_s_waitcnt(waitcnt_imm(LD_PER_STEP * (kStages - 2), 0));
+    }
     __syncthreads();
-    if (dma) issue(kt + 2, stage);
-    if (next) read_frags(stage ^ 1, 0, 0);
-    mfmas(1);
+    __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-    for (int i = 0; i < 16; ++i) {
-      __builtin_amdgcn_sched_group_barrier(kSchedMfma, 1, 0);
-      __builtin_amdgcn_sched_group_barrier(kSchedVmem, 1, 0);
-      if (i < 8) __builtin_amdgcn_sched_group_barrier(kSchedDsRead, 1, 0);
+    for (int i = 0; i < MI * NI; ++i) {
+      mfma1((NSUB - 1) & 1, i);
+      if (dma && i < LD_PER_STEP) dma1(kt + kStages, stage, i);
+      if (next && i < NFRAG) read1(next_stage, 0, 0, i);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    if (dma) {
+#pragma unroll
+      for (int d = MI * NI; d < LD_PER_STEP; ++d) dma1(kt + kStages, stage, d);
     }
     __builtin_amdgcn_sched_barrier(0);
   };
-  auto kstep = [&](int kt, bool dma, bool next) __attribute__((always_inline)) {
-    const int stage = kt & 1;
-    substep(stage, 0);
-    substep(stage, 1);
-    substep(stage, 2);
-    last_substep(kt, stage, dma, next);
+  auto kstep = [&](int kt, int stage, int next_stage, bool dma, bool next,
+                   bool drain) __attribute__((always_inline)) {
+#pragma unroll
+    for (int s = 0; s + 1 < NSUB; ++s) substep(stage, s);
+    last_substep(kt, stage, next_stage, dma, next, drain);
   };
 
   const int KT = p.K / kBK;
-  issue(0, 0);
-  if (KT > 1) {
-    issue(1, 1);
-    // step 0's 2 * LD_PER_WAVE loads of this wave landed (step 1's may be in flight)
-    __builtin_amdgcn_s_waitcnt(waitcnt_imm(2 * LD_PER_WAVE, 15));
+  // Prologue: the first min(KT, kStages) steps in flight, step 0 landed.
+  const int pre = KT < kStages ? KT : kStages;
+  for (int i = 0; i < pre; ++i) issue(i, i);
+  if (pre == kStages) {
+    __builtin_amdgcn_s_waitcnt(waitcnt_imm(LD_PER_STEP * (kStages - 1), 15));
   } else {
     __builtin_amdgcn_s_waitcnt(waitcnt_imm(0, 15));
   }
@@ -280,10 +327,20 @@ __global__ __launch_bounds__(kGemmThreads, 1) void gemm_nt_kernel(const GemmPara
   __builtin_amdgcn_s_waitcnt(waitcnt_imm(63, 0));
   __builtin_amdgcn_sched_barrier(0);
 
-  int kt = 0;
-  for (; kt + 2 < KT; ++kt) kstep(kt, true, true);
-  if (kt + 1 < KT) kstep(kt++, false, true);
-  kstep(kt, false, false);
+  // Steady state: every step refills its stage with step kt + kStages.  The tail
+  // steps issue nothing and drain the counters (their waits use vmcnt(0)).
+  int kt = 0, stage = 0;
+  for (; kt + kStages < KT; ++kt) {
+    const int nxt = stage + 1 == kStages ? 0 : stage + 1;
+    kstep(kt, stage, nxt, true, true, false);
+    stage = nxt;
+  }
+  for (; kt + 1 < KT; ++kt) {
+    const int nxt = stage + 1 == kStages ? 0 : stage + 1;
+    kstep(kt, stage, nxt, false, true, true);
+    stage = nxt;
+  }
+  kstep(kt, stage, 0, false, false, true);
 
   // ---- epilogue --------------------------------------------------------------
   const int hi = lane >> 5;

@@ -8,13 +8,13 @@
 namespace cdx {
 namespace {
 
-template <ALoad AL, Epi EP>
+template <ALoad AL, Epi EP, class Cfg = DefaultCfg>
 int launch(GemmParams p, hipStream_t s, const char* name) {
-  p.nt_count = (p.N + kBN - 1) / kBN;
+  p.nt_count = (p.N + Cfg::BN - 1) / Cfg::BN;
   const int64_t nb = (int64_t)p.mt_count * p.nt_count;
   if (nb == 0) return CDX_OK;
   if (nb > INT32_MAX) return fail(CDX_EUNSUPPORTED, "%s: problem too large (%lld tiles)", name, (long long)nb);
-  gemm_nt_kernel<AL, EP><<<dim3((unsigned)nb), dim3(kGemmThreads), 0, s>>>(p);
+  gemm_nt_kernel<Cfg, AL, EP><<<dim3((unsigned)nb), dim3(kGemmThreads), 0, s>>>(p);
   return check_launch(name);
 }
 
