@@ -9,9 +9,13 @@ Interfaces follow the reference:
 The projection is one MFMA contraction over K = 2H: [x | mu_prev] @ W_pack^T with
 W_pack = [[Wq; Wk; Wv] | [Wmu_q; Wmu_k; Wmu_v]] packed once (cached per parameter
 version) instead of being concatenated on every forward (attention.py:122-124).  q,
-k and v are column slices of the packed [T, Nq*D + 2*Nkv*D] output.  Everything
-after the projection — QK RMSNorm, RoPE, KV cache, GQA SDPA, o_proj — runs as
-PyTorch-ROCm ops, exactly as the reference orders them (attention.py:133-181).
+k and v are column slices of the packed [T, Nq*D + 2*Nkv*D] output.
+
+ComplexityAttention.forward goes one step further for head dims 32/64/128: the
+per-head QK RMSNorm and RoPE (attention.py:138-155) run in the projection kernel's
+epilogue (cdx_mu_qkv_rope_fwd), which writes q, k, v head-major, in fp32 up to one
+final rounding.  The KV cache, GQA SDPA and o_proj stay PyTorch-ROCm ops in the
+reference's order (attention.py:157-181).
 """
 
 from __future__ import annotations
@@ -71,6 +75,44 @@ def mu_qkv_project(x: torch.Tensor, mu: Optional[torch.Tensor], w_pack: torch.Te
                                            w_pack.stride(0), M, H, N, out.data_ptr(), N,
                                            nat.stream_of(x)), "cdx_mu_qkv_fwd")
     return out
+
+
+def mu_qkv_rope(x: torch.Tensor, mu: Optional[torch.Tensor], w_pack: torch.Tensor, H: int, nq: int,
+                nkv: int, hd: int, q_norm_w: Optional[torch.Tensor], k_norm_w: Optional[torch.Tensor],
+                eps: float, cos_sin: torch.Tensor, pos0: int = 0
+                ) -> Tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
+    """(q, k, v) head-major [B, heads, S, hd] from x [B, S, H] (cdx_mu_qkv_rope_fwd):
+    the mu-QKV projection with per-head RMSNorm of q and k (weights q_norm_w /
+    k_norm_w, None = no norm) and RoPE at positions pos0 .. pos0+S-1 fused into one
+    kernel.  cos_sin is the fp32 [n_pos, hd/2, 2] table of RotaryEmbedding."""
+    nat.require_device(x, mu, w_pack, q_norm_w, k_norm_w, what="mu_qkv_rope")
+    B, S, _ = x.shape
+    x2, ldx = _rows_view(x, H)
+    if ldx == 0:
+        x2, ldx = x.contiguous(), H
+    if mu is not None:
+        mu = mu.expand(B, S, H) if mu.shape[:-1] != (B, S) else mu
+        mu2, ldmu = _rows_view(mu, H)
+    else:
+        mu2, ldmu = None, 0
+    if w_pack.stride(-1) != 1:
+        raise ValueError("mu_qkv_rope: packed weight must be unit-stride in K")
+    if cos_sin.dtype != torch.float32 or not cos_sin.is_contiguous() or cos_sin.device != x.device:
+        raise ValueError("mu_qkv_rope: cos_sin must be a contiguous fp32 table on the input's device")
+    if (q_norm_w is None) != (k_norm_w is None):
+        raise ValueError("mu_qkv_rope: pass both QK norm weights or neither")
+    if q_norm_w is not None:
+        q_norm_w = q_norm_w.to(x.dtype).contiguous()
+        k_norm_w = k_norm_w.to(x.dtype).contiguous()
+    q = torch.empty(B, nq, S, hd, dtype=x.dtype, device=x.device)
+    k = torch.empty(B, nkv, S, hd, dtype=x.dtype, device=x.device)
+    v = torch.empty(B, nkv, S, hd, dtype=x.dtype, device=x.device)
+    with nat.launch_region("mu_qkv", x.device, M=B * S, H=H, N=(nq + 2 * nkv) * hd, mu=mu2 is not None):
+        nat.check(nat.lib().cdx_mu_qkv_rope_fwd(
+            x2.data_ptr(), ldx, nat.ptr(mu2), ldmu, w_pack.data_ptr(), w_pack.stride(0), B, S, H, nq, nkv, hd,
+            nat.ptr(q_norm_w), nat.ptr(k_norm_w), float(eps), cos_sin.data_ptr(), cos_sin.shape[0], pos0,
+            q.data_ptr(), k.data_ptr(), v.data_ptr(), nat.stream_of(x)), "cdx_mu_qkv_rope_fwd")
+    return q, k, v
 
 
 def fused_mu_qkv_projection(x: torch.Tensor, mu: Optional[torch.Tensor], wq: torch.Tensor,
@@ -178,27 +220,45 @@ class ComplexityAttention(nn.Module):
             w = w[:, : self.hidden_size]
         return mu_qkv_project(hidden_states, mu_prev, w, self.hidden_size)
 
+    @property
+    def fused_prologue(self) -> bool:
+        """Whether QK-norm + RoPE run inside the projection kernel (cdx_mu_qkv_rope_fwd
+        handles head dims 32, 64 and 128 and H a multiple of 64)."""
+        return self.head_dim in (32, 64, 128) and self.hidden_size % 64 == 0
+
     def forward(self, hidden_states: torch.Tensor, attention_mask: Optional[torch.Tensor] = None,
                 past_key_value: Optional[Tuple[torch.Tensor, torch.Tensor]] = None,
                 use_cache: bool = False, mu_prev: Optional[torch.Tensor] = None):
         forward_only("ComplexityAttention", hidden_states, mu_prev, *self.parameters())
         B, S, _ = hidden_states.shape
         D = self.head_dim
-        q_dim, kv_dim = self.num_heads * D, self.num_kv_heads * D
-        qkv = self.project_qkv(hidden_states, mu_prev)
-        q = qkv[..., :q_dim].view(B, S, self.num_heads, D).transpose(1, 2)
-        k = qkv[..., q_dim:q_dim + kv_dim].view(B, S, self.num_kv_heads, D).transpose(1, 2)
-        v = qkv[..., q_dim + kv_dim:].view(B, S, self.num_kv_heads, D).transpose(1, 2)
-        if self.use_qk_norm:
-            q = self.q_norm(q)
-            k = self.k_norm(k)
-        kv_seq_len = S + (past_key_value[0].shape[2] if past_key_value is not None else 0)
-        cos, sin = self.rotary_emb(kv_seq_len)
-        cos = cos.to(q.device, dtype=q.dtype)
-        sin = sin.to(q.device, dtype=q.dtype)
-        if past_key_value is not None:
-            cos, sin = cos[kv_seq_len - S:], sin[kv_seq_len - S:]
-        q, k = apply_rotary_pos_emb(q, k, cos, sin)
+        past_len = past_key_value[0].shape[2] if past_key_value is not None else 0
+        if self.fused_prologue:
+            # Projection, head split, QK RMSNorm and RoPE in one kernel (attention.py:120-155).
+            w = self._cache.get(self)
+            if mu_prev is None:
+                w = w[:, : self.hidden_size]
+            table = self.rotary_emb.cos_sin_table(past_len + S, hidden_states.device)
+            qn = (self.q_norm.weight, self.k_norm.weight) if self.use_qk_norm else (None, None)
+            eps = self.q_norm.eps if self.use_qk_norm else 0.0
+            q, k, v = mu_qkv_rope(hidden_states, mu_prev, w, self.hidden_size, self.num_heads,
+                                  self.num_kv_heads, D, qn[0], qn[1], eps, table, past_len)
+        else:
+            q_dim, kv_dim = self.num_heads * D, self.num_kv_heads * D
+            qkv = self.project_qkv(hidden_states, mu_prev)
+            q = qkv[..., :q_dim].view(B, S, self.num_heads, D).transpose(1, 2)
+            k = qkv[..., q_dim:q_dim + kv_dim].view(B, S, self.num_kv_heads, D).transpose(1, 2)
+            v = qkv[..., q_dim + kv_dim:].view(B, S, self.num_kv_heads, D).transpose(1, 2)
+            if self.use_qk_norm:
+                q = self.q_norm(q)
+                k = self.k_norm(k)
+            kv_seq_len = S + past_len
+            cos, sin = self.rotary_emb(kv_seq_len)
+            cos = cos.to(q.device, dtype=q.dtype)
+            sin = sin.to(q.device, dtype=q.dtype)
+            if past_key_value is not None:
+                cos, sin = cos[kv_seq_len - S:], sin[kv_seq_len - S:]
+            q, k = apply_rotary_pos_emb(q, k, cos, sin)
         if past_key_value is not None:
             k = torch.cat([past_key_value[0], k], dim=2)
             v = torch.cat([past_key_value[1], v], dim=2)
@@ -217,4 +277,4 @@ class ComplexityAttention(nn.Module):
 MuGuidedAttention = ComplexityAttention
 
 __all__ = ["ComplexityAttention", "MuGuidedAttention", "FusedMuQKVProjection", "fused_mu_qkv_projection",
-           "mu_qkv_project"]
+           "mu_qkv_project", "mu_qkv_rope"]

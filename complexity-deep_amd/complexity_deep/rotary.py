@@ -36,6 +36,22 @@ class RotaryEmbedding(nn.Module):
             self.max_seq_len = seq_len
         return self.cos_cached[:seq_len], self.sin_cached[:seq_len]
 
+    def cos_sin_table(self, n_pos: int, device: torch.device) -> torch.Tensor:
+        """fp32 [n, dim/2, 2] table of (cos, sin)(p * inv_freq[j]) for p < n >= n_pos, the
+        form the fused QKV + RoPE kernel reads.  The angles are the fp32 products of
+        _build_cache; the table stays fp32 whatever dtype the module was cast to.
+        Cached per device and inv_freq version; grows geometrically."""
+        inv = self.inv_freq
+        key = (device, inv.data_ptr(), inv._version, inv.dtype)
+        cached = getattr(self, "_cs_table", None)
+        if cached is None or cached[0] != key or cached[1].shape[0] < n_pos:
+            n = max(n_pos, self.max_seq_len, 2 * cached[1].shape[0] if cached is not None and cached[0] == key else 0)
+            pos = torch.arange(n, device=device, dtype=torch.float32)
+            angles = torch.outer(pos, inv.to(device=device, dtype=torch.float32))
+            table = torch.stack([angles.cos(), angles.sin()], dim=-1).contiguous()
+            self._cs_table = (key, table)
+        return self._cs_table[1]
+
 
 def rotate_half(x: torch.Tensor) -> torch.Tensor:
     half = x.shape[-1] // 2

@@ -41,7 +41,23 @@
 namespace cdx {
 
 enum class ALoad { kDense, kConcat, kGather };
-enum class Epi { kStore, kSwiGLU, kScatter };
+enum class Epi { kStore, kSwiGLU, kScatter, kQKRope };
+
+// Parameters of the kQKRope epilogue (mu-QKV with QK RMSNorm and RoPE fused): the
+// packed [M, (nq + 2 nkv) * HD] projection is never stored; q, k and v go straight
+// to head-major [B, heads, S, HD] buffers, q and k normalised and rotated.
+struct QKRopeParams {
+  int64_t S;                 // tokens per sequence; row m is token (m / S, m % S)
+  int32_t nq, nkv;           // query and key/value heads
+  const uint16_t* q_norm_w;  // [HD] bf16, nullptr = no QK RMSNorm
+  const uint16_t* k_norm_w;  // [HD] bf16
+  float eps;
+  const float* cos_sin;      // [pos][HD/2] (cos, sin) pairs, fp32
+  int64_t pos0;              // position of token s = 0 (KV-cache length)
+  uint16_t* q_out;           // [B, nq, S, HD]
+  uint16_t* k_out;           // [B, nkv, S, HD]
+  uint16_t* v_out;           // [B, nkv, S, HD]
+};
 
 struct GemmParams {
   // A operand
@@ -67,6 +83,7 @@ struct GemmParams {
   // grid decomposition
   int32_t mt_count;  // number of M tiles (upper bound for grouped GEMMs)
   int32_t nt_count;
+  QKRopeParams qk;  // kQKRope epilogue only
 };
 
 constexpr int kBM = 256;
@@ -110,7 +127,7 @@ __device__ __forceinline__ void dma16(const uint16_t* g, uint8_t* lds_block) {
                                    (__attribute__((address_space(3))) void*)lds_block, 16, 0, 0);
 }
 
-template <class Cfg, ALoad AL, Epi EP>
+template <class Cfg, ALoad AL, Epi EP, int HD = 0>
 __global__ __launch_bounds__(kGemmThreads, Cfg::MINB) void gemm_nt_kernel(const GemmParams p) {
   constexpr int kBN = Cfg::BN, kBK = Cfg::BK, kStages = Cfg::STAGES;
   constexpr int ROW_BYTES = kBK * 2;                // bytes per tile row in LDS
@@ -344,6 +361,98 @@ __global__ __launch_bounds__(kGemmThreads, Cfg::MINB) void gemm_nt_kernel(const 
 
   // ---- epilogue --------------------------------------------------------------
   const int hi = lane >> 5;
+  if constexpr (EP == Epi::kQKRope) {
+    // Head-wise epilogue.  A wave's WN columns hold WN / HD whole heads; for row m
+    // a lane holds half of a head's HD values (its partner lane l ^ 32 the rest),
+    // and both elements of every RoPE pair (c, c + HD/2): 32-column blocks nb and
+    // nb ^ (BPH/2) for HD >= 64, accumulator slots v and v ^ 8 for HD = 32.
+    static_assert(HD == 32 || HD == 64 || HD == 128, "head dim must be 32, 64 or 128");
+    constexpr int BPH = HD / 32, HPW = WN / HD, HALF = HD / 2;
+    const QKRopeParams& q = p.qk;
+    const int qd = q.nq * HD, kvd = q.nkv * HD;
+#pragma unroll
+    for (int hb = 0; hb < HPW; ++hb) {
+      const int c0 = n0 + wn * WN + hb * HD;  // first global column of this head
+      if (c0 >= p.N) continue;
+      const int kind = c0 < qd ? 0 : (c0 < qd + kvd ? 1 : 2);  // q, k, v
+      const int head = kind == 0 ? c0 / HD : (kind == 1 ? (c0 - qd) / HD : (c0 - qd - kvd) / HD);
+      const int nheads = kind == 0 ? q.nq : q.nkv;
+      uint16_t* obase = kind == 0 ? q.q_out : (kind == 1 ? q.k_out : q.v_out);
+      const uint16_t* nw = kind == 0 ? q.q_norm_w : (kind == 1 ? q.k_norm_w : nullptr);
+#pragma unroll
+      for (int mi = 0; mi < MI; ++mi) {
+        const int64_t gm = m0 + wm * WM + mi * 32 + (lane & 31);
+        float x[BPH][16];
+#pragma unroll
+        for (int nb = 0; nb < BPH; ++nb)
+#pragma unroll
+          for (int v = 0; v < 16; ++v) x[nb][v] = acc[mi][hb * BPH + nb][v];
+        if (kind != 2 && nw != nullptr) {
+          // RMSNorm over the head: this lane's half plus its partner's.
+          float ss = 0.f;
+#pragma unroll
+          for (int nb = 0; nb < BPH; ++nb)
+#pragma unroll
+            for (int v = 0; v < 16; ++v) ss += x[nb][v] * x[nb][v];
+          ss += __shfl_xor(ss, 32, 64);
+          const float r = rsqrtf(ss / (float)HD + q.eps);
+#pragma unroll
+          for (int nb = 0; nb < BPH; ++nb)
+#pragma unroll
+            for (int g = 0; g < 4; ++g) {
+              const uint2 wv = *reinterpret_cast<const uint2*>(nw + nb * 32 + 8 * g + 4 * hi);
+              const float w4[4] = {__uint_as_float(wv.x << 16), __uint_as_float(wv.x & 0xffff0000u),
+                                   __uint_as_float(wv.y << 16), __uint_as_float(wv.y & 0xffff0000u)};
+#pragma unroll
+              for (int j = 0; j < 4; ++j) x[nb][4 * g + j] = w4[j] * (x[nb][4 * g + j] * r);
+            }
+        }
+        if (gm >= m_end) continue;
+        const int64_t b = gm / q.S, s = gm - b * q.S;
+        uint16_t* orow = obase + (((b * nheads + head) * q.S) + s) * HD;
+        auto store4 = [&](int c, float y0, float y1, float y2, float y3) __attribute__((always_inline)) {
+          uint2 o;
+          o.x = pack_bf16x2(y0, y1);
+          o.y = pack_bf16x2(y2, y3);
+          *reinterpret_cast<uint2*>(orow + c) = o;
+        };
+        if (kind == 2) {
+#pragma unroll
+          for (int nb = 0; nb < BPH; ++nb)
+#pragma unroll
+            for (int g = 0; g < 4; ++g)
+              store4(nb * 32 + 8 * g + 4 * hi, x[nb][4 * g], x[nb][4 * g + 1], x[nb][4 * g + 2], x[nb][4 * g + 3]);
+          continue;
+        }
+        // RoPE on each pair (c, c + HALF), c < HALF, sharing the angle of index c:
+        //   y[c] = x[c] cos - x[c + HALF] sin,  y[c + HALF] = x[c + HALF] cos + x[c] sin.
+        const float2* cs = reinterpret_cast<const float2*>(q.cos_sin) + (q.pos0 + s) * HALF;
+        constexpr int NB_LO = HD >= 64 ? BPH / 2 : 1;  // 32-column blocks holding first-half columns
+        constexpr int G_LO = HD >= 64 ? 4 : 2;         // groups of 4 slots per block in the first half
+#pragma unroll
+        for (int nb = 0; nb < NB_LO; ++nb)
+#pragma unroll
+          for (int g = 0; g < G_LO; ++g) {
+            const int c = nb * 32 + 8 * g + 4 * hi;  // first-half column, c % 4 == 0
+            const float4 t01 = *reinterpret_cast<const float4*>(cs + c);
+            const float4 t23 = *reinterpret_cast<const float4*>(cs + c + 2);
+            const float cv[4] = {t01.x, t01.z, t23.x, t23.z};
+            const float sv[4] = {t01.y, t01.w, t23.y, t23.w};
+            float lo[4], up[4];
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+              const float a = x[nb][4 * g + j];
+              const float bq = HD >= 64 ? x[nb + BPH / 2][4 * g + j] : x[nb][4 * g + j + 8];
+              lo[j] = a * cv[j] - bq * sv[j];
+              up[j] = bq * cv[j] + a * sv[j];
+            }
+            store4(c, lo[0], lo[1], lo[2], lo[3]);
+            store4(c + HALF, up[0], up[1], up[2], up[3]);
+          }
+      }
+    }
+    return;
+  }
 #pragma unroll
   for (int mi = 0; mi < MI; ++mi) {
     const int64_t gm = m0 + wm * WM + mi * 32 + (lane & 31);

@@ -1,5 +1,7 @@
 // C-ABI entry points built on the MFMA tile engine (cdx_gemm.h):
 //   cdx_mu_qkv_fwd       piece 2: one K = 2H contraction over [x | mu_prev]
+//   cdx_mu_qkv_rope_fwd  the same contraction with QK RMSNorm + RoPE fused into the
+//                        epilogue, writing head-major q, k, v
 //   cdx_moe_swiglu_fwd   piece 1b: gather + gate/up + SwiGLU, then down + scatter,
 //                        with the shared expert folded into both passes
 //   cdx_grouped_gemm_fwd plain grouped GEMM over expert segments
@@ -8,13 +10,13 @@
 namespace cdx {
 namespace {
 
-template <ALoad AL, Epi EP, class Cfg = DefaultCfg>
+template <ALoad AL, Epi EP, class Cfg = DefaultCfg, int HD = 0>
 int launch(GemmParams p, hipStream_t s, const char* name) {
   p.nt_count = (p.N + Cfg::BN - 1) / Cfg::BN;
   const int64_t nb = (int64_t)p.mt_count * p.nt_count;
   if (nb == 0) return CDX_OK;
   if (nb > INT32_MAX) return fail(CDX_EUNSUPPORTED, "%s: problem too large (%lld tiles)", name, (long long)nb);
-  gemm_nt_kernel<Cfg, AL, EP><<<dim3((unsigned)nb), dim3(kGemmThreads), 0, s>>>(p);
+  gemm_nt_kernel<Cfg, AL, EP, HD><<<dim3((unsigned)nb), dim3(kGemmThreads), 0, s>>>(p);
   return check_launch(name);
 }
 
@@ -160,4 +162,77 @@ extern "C" int cdx_grouped_gemm_fwd(const uint16_t* a, int64_t T, int32_t K, int
   p.ldc = N;
   p.mt_count = (int32_t)(cdiv(T, kBM) + E);
   return launch<ALoad::kDense, Epi::kStore>(p, reinterpret_cast<hipStream_t>(stream), name);
+}
+
+extern "C" int cdx_mu_qkv_rope_fwd(const uint16_t* x, int64_t ldx, const uint16_t* mu, int64_t ldmu,
+                                   const uint16_t* w, int64_t ldw, int64_t B, int64_t S, int32_t H,
+                                   int32_t nq, int32_t nkv, int32_t hd, const uint16_t* q_norm_w,
+                                   const uint16_t* k_norm_w, float eps, const float* cos_sin,
+                                   int64_t n_pos, int64_t pos0, uint16_t* q_out, uint16_t* k_out,
+                                   uint16_t* v_out, void* stream) {
+  using namespace cdx;
+  clear_error();
+  const char* name = "cdx_mu_qkv_rope_fwd";
+  if (B < 0 || S < 0 || H <= 0 || nq <= 0 || nkv <= 0 || pos0 < 0 || n_pos < 0)
+    return fail(CDX_EINVAL, "%s: bad shape B=%lld S=%lld H=%d nq=%d nkv=%d", name, (long long)B, (long long)S,
+                H, nq, nkv);
+  if (hd != 32 && hd != 64 && hd != 128)
+    return fail(CDX_EUNSUPPORTED, "%s: head dim %d must be 32, 64 or 128", name, hd);
+  if (H % 64 != 0) return fail(CDX_EUNSUPPORTED, "%s: H=%d must be a multiple of 64", name, H);
+  if ((q_norm_w == nullptr) != (k_norm_w == nullptr))
+    return fail(CDX_EINVAL, "%s: q and k norm weights must both be given or both be NULL", name);
+  if (!(eps >= 0.f)) return fail(CDX_EINVAL, "%s: eps must be >= 0", name);
+  const int64_t M = B * S;
+  const int64_t N = (int64_t)(nq + 2 * nkv) * hd;
+  const int64_t K = mu ? 2 * (int64_t)H : (int64_t)H;
+  if (N > INT32_MAX) return fail(CDX_EUNSUPPORTED, "%s: too many heads", name);
+  if (ldx < H || ldw < K || (mu && ldmu != 0 && ldmu < H))
+    return fail(CDX_EINVAL, "%s: leading dimension too small", name);
+  if (ldx % 8 || ldw % 8 || (mu && ldmu % 8))
+    return fail(CDX_EUNSUPPORTED, "%s: leading dimensions must be multiples of 8", name);
+  if (M == 0) return CDX_OK;
+  if (pos0 + S > n_pos)
+    return fail(CDX_EINVAL, "%s: cos/sin table has %lld positions, needs %lld", name, (long long)n_pos,
+                (long long)(pos0 + S));
+  if (!x || !w || !cos_sin || !q_out || !k_out || !v_out) return fail(CDX_EINVAL, "%s: null pointer", name);
+  if (!aligned16(x) || !aligned16(w) || !aligned16(cos_sin) || !aligned16(q_out) || !aligned16(k_out) ||
+      !aligned16(v_out) || (mu && !aligned16(mu)) || (q_norm_w && (!aligned16(q_norm_w) || !aligned16(k_norm_w))))
+    return fail(CDX_EUNSUPPORTED, "%s: pointers must be 16-byte aligned", name);
+  GemmParams p{};
+  p.a = x;
+  p.lda = ldx;
+  p.a2 = mu;
+  p.lda2 = ldmu;
+  p.k_split = H;
+  p.E = 1;
+  p.M = M;
+  p.b = w;
+  p.ldb = ldw;
+  p.N = (int32_t)N;
+  p.K = (int32_t)K;
+  p.qk.S = S;
+  p.qk.nq = nq;
+  p.qk.nkv = nkv;
+  p.qk.q_norm_w = q_norm_w;
+  p.qk.k_norm_w = k_norm_w;
+  p.qk.eps = eps;
+  p.qk.cos_sin = cos_sin;
+  p.qk.pos0 = pos0;
+  p.qk.q_out = q_out;
+  p.qk.k_out = k_out;
+  p.qk.v_out = v_out;
+  if (cdiv(M, kBM) > INT32_MAX) return fail(CDX_EUNSUPPORTED, "%s: M too large", name);
+  p.mt_count = (int32_t)cdiv(M, kBM);
+  hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  switch (hd) {
+    case 32:
+      return mu ? launch<ALoad::kConcat, Epi::kQKRope, DefaultCfg, 32>(p, st, name)
+                : launch<ALoad::kDense, Epi::kQKRope, DefaultCfg, 32>(p, st, name);
+    case 64:
+      return mu ? launch<ALoad::kConcat, Epi::kQKRope, DefaultCfg, 64>(p, st, name)
+                : launch<ALoad::kDense, Epi::kQKRope, DefaultCfg, 64>(p, st, name);
+    default:
+      return mu ? launch<ALoad::kConcat, Epi::kQKRope, DefaultCfg, 128>(p, st, name)
+                : launch<ALoad::kDense, Epi::kQKRope, DefaultCfg, 128>(p, st, name);
+  }
 }

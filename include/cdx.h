@@ -171,6 +171,33 @@ int cdx_mu_qkv_fwd(const uint16_t* x_dev, int64_t ldx, const uint16_t* mu_dev, i
                    const uint16_t* w_pack_dev, int64_t ldw, int64_t M, int32_t H, int32_t N,
                    uint16_t* out_dev, int64_t ldo, void* stream);
 
+/*
+ * mu-QKV projection with the attention prologue fused into its epilogue:
+ *   [q | k | v] = [x | mu] @ w_pack^T              (as cdx_mu_qkv_fwd; N = (nq + 2 nkv) hd)
+ *   q_h = RoPE(q_norm_w * q_h / rms(q_h))          per head, per token; likewise k
+ *   v_h = v_h
+ * and writes q, k, v head-major: q_out [B, nq, S, hd], k_out / v_out [B, nkv, S, hd]
+ * (row m = b * S + s of x is token s of sequence b).  The packed projection never
+ * reaches memory; the norm and rotation run in fp32 on the accumulators and each
+ * output is rounded to bf16 once.
+ *   rms(z)   = sqrt(mean(z^2) + eps) over the hd values of the head.
+ *   RoPE     y[c] = z[c] cos(t_c) - z[c + hd/2] sin(t_c)   for c <  hd/2
+ *            y[c] = z[c] cos(t_c) + z[c - hd/2] sin(t_c)   for c >= hd/2
+ *            with (cos, sin)(t_c) = cos_sin[pos0 + s][c mod hd/2], fp32 pairs, a table of
+ *            n_pos >= pos0 + S positions (pos0 = tokens already in the KV cache).
+ * q_norm_w / k_norm_w ([hd] bf16) both NULL: no QK norm.  hd must be 32, 64 or 128
+ * and H a multiple of 64.  mu / ldmu / w_pack / ldw as in cdx_mu_qkv_fwd.
+ *
+ * Replaces: core/attention.py:120-155 (cat + three F.linear, head split, q_norm /
+ * k_norm, rotary tables and apply_rotary_pos_emb), core/rotary.py:57-86.
+ */
+int cdx_mu_qkv_rope_fwd(const uint16_t* x_dev, int64_t ldx, const uint16_t* mu_dev, int64_t ldmu,
+                        const uint16_t* w_pack_dev, int64_t ldw, int64_t B, int64_t S, int32_t H,
+                        int32_t nq, int32_t nkv, int32_t hd, const uint16_t* q_norm_w_dev,
+                        const uint16_t* k_norm_w_dev, float eps, const float* cos_sin_dev,
+                        int64_t n_pos, int64_t pos0, uint16_t* q_out_dev, uint16_t* k_out_dev,
+                        uint16_t* v_out_dev, void* stream);
+
 #ifdef __cplusplus
 }
 #endif
