@@ -51,6 +51,19 @@ def log(*a):
     print(*a, file=sys.stderr, flush=True)
 
 
+def measured_traffic(workload: str) -> dict:
+    """HBM bytes per launch of each hot-path kernel, from the committed rocprofv3
+    FETCH_SIZE / WRITE_SIZE runs of this workload (profiles/hbm_traffic_<workload>.json,
+    each counter scaled by its reading for a 1 GiB copy).  Empty if none is committed."""
+    path = REPO / "profiles" / f"hbm_traffic_{workload.replace('-', '_')}.json"
+    try:
+        with open(path) as f:
+            data = json.load(f)
+    except (OSError, ValueError):
+        return {}
+    return {k: v["hbm_bytes_per_launch"] for k, v in data.get("kernels", {}).items()}
+
+
 # ---------------------------------------------------------------------------
 # algorithmic work per entry-point call (the units roofline.achieved is priced on)
 # ---------------------------------------------------------------------------
@@ -283,6 +296,9 @@ def main() -> int:
     ap.add_argument("--no-cpu-baseline", action="store_true", help="skip the CPU oracle timing")
     ap.add_argument("--cpu-seqs", type=int, default=1, help="sequences of 2048 tokens in the CPU sample")
     ap.add_argument("--no-kernel-timing", action="store_true", help="do not record per-launch events")
+    ap.add_argument("--copy-calibration", action="store_true",
+                    help="first run one plain 1 GiB device copy (read 1 GiB, write 1 GiB): the reference "
+                         "dispatch that scales FETCH_SIZE / WRITE_SIZE counter runs")
     args = ap.parse_args()
 
     world = int(os.environ.get("WORLD_SIZE", "1"))
@@ -299,6 +315,13 @@ def main() -> int:
     nat.lib()
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
+    if args.copy_calibration:
+        src = torch.empty(1 << 30, dtype=torch.uint8, device=dev).fill_(1)
+        dst = torch.empty_like(src)
+        torch.cuda.synchronize()
+        dst.copy_(src)
+        torch.cuda.synchronize()
+        del src, dst
     log(f"device: {torch.cuda.get_device_name(dev)}; workload {args.workload}")
     step, tokens, config, dominant, ctx = WORKLOADS[args.workload](args, dev)
 
@@ -333,9 +356,12 @@ def main() -> int:
     dom = next((d for d in dominant if d in kernels), None)
     if dom is not None:
         k = kernels[dom]
+        traffic = measured_traffic(args.workload)
         roofline = {"kernel": dom, "bound": k["bound"], "achieved": k["achieved"],
                     "peak": PEAK_BF16_TFLOPS if k["bound"] == "mfma" else PEAK_HBM_GBS,
-                    "unit": k["unit"], "frac": k["frac"], "traffic": None,
+                    "unit": k["unit"], "frac": k["frac"], "traffic": traffic.get(dom),
+                    "traffic_source": f"profiles/hbm_traffic_{args.workload.replace('-', '_')}.json"
+                    if dom in traffic else None,
                     "work_per_launch": k["work_per_launch"], "avg_launch_us": k["avg_us"],
                     "timing": "HIP events around each launch on its stream, over the timed steps"}
 
