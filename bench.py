@@ -82,6 +82,10 @@ def work_of(name: str, s: dict):
         return float(rows * (4 if s["store_residual"] else 3) + 2 * s["H"]), "byte"
     if name == "rmsnorm":
         return float(2 * s["T"] * s["H"] * 2 + 2 * s["H"]), "byte"
+    if name == "attention":
+        # causal: query s sees s + 1 keys; QK^T and PV are 2 * D FLOP per (query, key) each
+        S = s["S"]
+        return 4.0 * s["B"] * s["nq"] * s["D"] * S * (S + 1) / 2, "flop"
     if name == "route_plan":
         # ids in; expert_id, perm, inv_perm out; the map is read once per token at most
         return float(s["T"] * (8 + 4 + 4 + 4) + 2 * 4 * (s["E"] + 1)), "byte"

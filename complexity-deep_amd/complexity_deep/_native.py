@@ -40,7 +40,9 @@ _SIGNATURES = {
                                       _vp]),
     "cdx_mu_qkv_rope_fwd": (ctypes.c_int, [_vp, _i64, _vp, _i64, _vp, _i64, _i64, _i64, _i32, _i32, _i32,
                                            _i32, _vp, _vp, ctypes.c_float, _vp, _i64, _i64, _vp, _vp, _vp,
-                                           _vp]),
+                                           _i64, _vp]),
+    "cdx_attention_fwd": (ctypes.c_int, [_vp, _vp, _vp, _i64, _i64, _i32, _i32, _i32, _i64, ctypes.c_float,
+                                         _vp, _vp]),
 }
 
 

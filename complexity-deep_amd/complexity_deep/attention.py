@@ -77,14 +77,40 @@ def mu_qkv_project(x: torch.Tensor, mu: Optional[torch.Tensor], w_pack: torch.Te
     return out
 
 
+def vt_ld_for(S: int) -> int:
+    """Row length of the transposed V layout (keys padded to a multiple of 64)."""
+    return (S + 63) // 64 * 64
+
+
+def vt_columns(S: int, device=None) -> torch.Tensor:
+    """Column of each token s in the transposed V layout: inside every group of 16 the
+    middle two groups of 4 swap places (the key order of the attention kernel's
+    P fragments)."""
+    s = torch.arange(S, device=device)
+    q = (s // 4) % 4
+    qs = torch.where(q == 1, 2, torch.where(q == 2, 1, q))
+    return (s // 16) * 16 + 4 * qs + s % 4
+
+
+def to_vt_layout(v: torch.Tensor) -> torch.Tensor:
+    """[B, h, S, D] -> the transposed layout [B, h, D, vt_ld] cdx_attention_fwd reads
+    (padding columns zero).  The model never calls this: the projection kernel writes
+    V in this layout directly."""
+    B, h, S, D = v.shape
+    vt = torch.zeros(B, h, D, vt_ld_for(S), dtype=v.dtype, device=v.device)
+    vt[..., vt_columns(S, v.device)] = v.transpose(-1, -2)
+    return vt
+
+
 def mu_qkv_rope(x: torch.Tensor, mu: Optional[torch.Tensor], w_pack: torch.Tensor, H: int, nq: int,
                 nkv: int, hd: int, q_norm_w: Optional[torch.Tensor], k_norm_w: Optional[torch.Tensor],
-                eps: float, cos_sin: torch.Tensor, pos0: int = 0
+                eps: float, cos_sin: torch.Tensor, pos0: int = 0, v_transposed: bool = False
                 ) -> Tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
     """(q, k, v) head-major [B, heads, S, hd] from x [B, S, H] (cdx_mu_qkv_rope_fwd):
     the mu-QKV projection with per-head RMSNorm of q and k (weights q_norm_w /
     k_norm_w, None = no norm) and RoPE at positions pos0 .. pos0+S-1 fused into one
-    kernel.  cos_sin is the fp32 [n_pos, hd/2, 2] table of RotaryEmbedding."""
+    kernel.  cos_sin is the fp32 [n_pos, hd/2, 2] table of RotaryEmbedding.
+    v_transposed=True returns V in the layout of to_vt_layout instead."""
     nat.require_device(x, mu, w_pack, q_norm_w, k_norm_w, what="mu_qkv_rope")
     B, S, _ = x.shape
     x2, ldx = _rows_view(x, H)
@@ -106,13 +132,48 @@ def mu_qkv_rope(x: torch.Tensor, mu: Optional[torch.Tensor], w_pack: torch.Tenso
         k_norm_w = k_norm_w.to(x.dtype).contiguous()
     q = torch.empty(B, nq, S, hd, dtype=x.dtype, device=x.device)
     k = torch.empty(B, nkv, S, hd, dtype=x.dtype, device=x.device)
-    v = torch.empty(B, nkv, S, hd, dtype=x.dtype, device=x.device)
+    if v_transposed:
+        vt_ld = vt_ld_for(S)
+        v = torch.empty(B, nkv, hd, vt_ld, dtype=x.dtype, device=x.device)
+        if vt_ld > S:
+            # Columns of the key positions S .. vt_ld-1 are masked but must be finite.
+            # The order inside a 16-group moves some of them below S, so clear from the
+            # last partial group on; the kernel then fills the columns of tokens < S.
+            v[..., (S // 16) * 16:].zero_()
+    else:
+        vt_ld = 0
+        v = torch.empty(B, nkv, S, hd, dtype=x.dtype, device=x.device)
     with nat.launch_region("mu_qkv", x.device, M=B * S, H=H, N=(nq + 2 * nkv) * hd, mu=mu2 is not None):
         nat.check(nat.lib().cdx_mu_qkv_rope_fwd(
             x2.data_ptr(), ldx, nat.ptr(mu2), ldmu, w_pack.data_ptr(), w_pack.stride(0), B, S, H, nq, nkv, hd,
             nat.ptr(q_norm_w), nat.ptr(k_norm_w), float(eps), cos_sin.data_ptr(), cos_sin.shape[0], pos0,
-            q.data_ptr(), k.data_ptr(), v.data_ptr(), nat.stream_of(x)), "cdx_mu_qkv_rope_fwd")
+            q.data_ptr(), k.data_ptr(), v.data_ptr(), vt_ld, nat.stream_of(x)), "cdx_mu_qkv_rope_fwd")
     return q, k, v
+
+
+def causal_attention(q: torch.Tensor, k: torch.Tensor, vt: torch.Tensor, scale: Optional[float] = None
+                     ) -> torch.Tensor:
+    """softmax(q k^T * scale, top-left causal) v for GQA heads (cdx_attention_fwd).
+
+    q [B, nq, S, D], k [B, nkv, S, D], vt = V in the transposed layout
+    [B, nkv, D, vt_ld] (to_vt_layout / mu_qkv_rope(v_transposed=True)).  Returns the
+    merged [B, S, nq * D] that o_proj consumes.  Equals
+    F.scaled_dot_product_attention(q, k.repeat_interleave(nq // nkv, 1),
+    v.repeat_interleave(nq // nkv, 1), is_causal=True) (core/attention.py:163-181)."""
+    nat.require_device(q, k, vt, what="causal_attention")
+    B, nq, S, D = q.shape
+    nkv = k.shape[1]
+    if k.shape != (B, nkv, S, D) or vt.shape[:3] != (B, nkv, D) or vt.shape[3] < S:
+        raise ValueError("causal_attention: q/k/vt shapes do not match")
+    if not (q.is_contiguous() and k.is_contiguous() and vt.is_contiguous()):
+        raise ValueError("causal_attention: q, k and vt must be contiguous")
+    scale = D ** -0.5 if scale is None else scale
+    out = torch.empty(B, S, nq * D, dtype=q.dtype, device=q.device)
+    with nat.launch_region("attention", q.device, B=B, S=S, nq=nq, D=D):
+        nat.check(nat.lib().cdx_attention_fwd(q.data_ptr(), k.data_ptr(), vt.data_ptr(), B, S, nq, nkv, D,
+                                              vt.shape[3], float(scale), out.data_ptr(), nat.stream_of(q)),
+                  "cdx_attention_fwd")
+    return out
 
 
 def fused_mu_qkv_projection(x: torch.Tensor, mu: Optional[torch.Tensor], wq: torch.Tensor,
@@ -233,6 +294,19 @@ class ComplexityAttention(nn.Module):
         B, S, _ = hidden_states.shape
         D = self.head_dim
         past_len = past_key_value[0].shape[2] if past_key_value is not None else 0
+        if self.fused_prologue and attention_mask is None and past_key_value is None and not use_cache \
+                and not (self.training and self.attention_dropout > 0):
+            # Whole attention on the kernels: fused projection (V written transposed) and
+            # the causal GQA kernel, whose output is already merged over heads.
+            w = self._cache.get(self)
+            if mu_prev is None:
+                w = w[:, : self.hidden_size]
+            table = self.rotary_emb.cos_sin_table(S, hidden_states.device)
+            qn = (self.q_norm.weight, self.k_norm.weight) if self.use_qk_norm else (None, None)
+            eps = self.q_norm.eps if self.use_qk_norm else 0.0
+            q, k, vt = mu_qkv_rope(hidden_states, mu_prev, w, self.hidden_size, self.num_heads,
+                                   self.num_kv_heads, D, qn[0], qn[1], eps, table, 0, v_transposed=True)
+            return self.o_proj(causal_attention(q, k, vt)), None
         if self.fused_prologue:
             # Projection, head split, QK RMSNorm and RoPE in one kernel (attention.py:120-155).
             w = self._cache.get(self)
@@ -277,4 +351,4 @@ class ComplexityAttention(nn.Module):
 MuGuidedAttention = ComplexityAttention
 
 __all__ = ["ComplexityAttention", "MuGuidedAttention", "FusedMuQKVProjection", "fused_mu_qkv_projection",
-           "mu_qkv_project", "mu_qkv_rope"]
+           "mu_qkv_project", "mu_qkv_rope", "causal_attention", "to_vt_layout", "vt_columns"]

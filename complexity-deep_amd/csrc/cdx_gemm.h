@@ -56,8 +56,22 @@ struct QKRopeParams {
   int64_t pos0;              // position of token s = 0 (KV-cache length)
   uint16_t* q_out;           // [B, nq, S, HD]
   uint16_t* k_out;           // [B, nkv, S, HD]
-  uint16_t* v_out;           // [B, nkv, S, HD]
+  uint16_t* v_out;           // [B, nkv, S, HD], or transposed (vt_ld > 0)
+  // vt_ld > 0: v_out is V transposed for the attention kernel, [B, nkv, HD, vt_ld]
+  // (vt_ld >= S, a multiple of 64), with token s stored at column vt_col(s).
+  int64_t vt_ld;
 };
+
+// Column of token s in the transposed V layout: inside every group of 16 tokens the
+// middle two quads swap places (s = 16 u + 4 q + j -> 16 u + 4 sigma(q) + j, sigma =
+// (0 2 1 3)).  The attention kernel's P fragments hold, per lane half, keys
+// {16 u + 4 h + j, 16 u + 8 + 4 h + j}; this order makes those eight keys one
+// contiguous 16-byte run of a V^T row.
+__host__ __device__ __forceinline__ int64_t vt_col(int64_t s) {
+  const int64_t q = (s >> 2) & 3;
+  const int64_t qs = q == 1 ? 2 : (q == 2 ? 1 : q);
+  return (s & ~int64_t(15)) + 4 * qs + (s & 3);
+}
 
 struct GemmParams {
   // A operand
@@ -417,6 +431,18 @@ __global__ __launch_bounds__(kGemmThreads, Cfg::MINB) void gemm_nt_kernel(const 
           *reinterpret_cast<uint2*>(orow + c) = o;
         };
         if (kind == 2) {
+          if (q.vt_ld > 0) {
+            // V^T: column vt_col(s) of rows d; 32 consecutive tokens per half wave.
+            uint16_t* vt = q.v_out + ((b * nheads + head) * HD) * q.vt_ld + vt_col(s);
+#pragma unroll
+            for (int nb = 0; nb < BPH; ++nb)
+#pragma unroll
+              for (int v = 0; v < 16; ++v) {
+                const int d = nb * 32 + 8 * (v >> 2) + 4 * hi + (v & 3);
+                vt[(int64_t)d * q.vt_ld] = f32_to_bf16_bits(x[nb][v]);
+              }
+            continue;
+          }
 #pragma unroll
           for (int nb = 0; nb < BPH; ++nb)
 #pragma unroll

@@ -169,7 +169,7 @@ extern "C" int cdx_mu_qkv_rope_fwd(const uint16_t* x, int64_t ldx, const uint16_
                                    int32_t nq, int32_t nkv, int32_t hd, const uint16_t* q_norm_w,
                                    const uint16_t* k_norm_w, float eps, const float* cos_sin,
                                    int64_t n_pos, int64_t pos0, uint16_t* q_out, uint16_t* k_out,
-                                   uint16_t* v_out, void* stream) {
+                                   uint16_t* v_out, int64_t vt_ld, void* stream) {
   using namespace cdx;
   clear_error();
   const char* name = "cdx_mu_qkv_rope_fwd";
@@ -190,6 +190,8 @@ extern "C" int cdx_mu_qkv_rope_fwd(const uint16_t* x, int64_t ldx, const uint16_
     return fail(CDX_EINVAL, "%s: leading dimension too small", name);
   if (ldx % 8 || ldw % 8 || (mu && ldmu % 8))
     return fail(CDX_EUNSUPPORTED, "%s: leading dimensions must be multiples of 8", name);
+  if (vt_ld < 0 || (vt_ld > 0 && (vt_ld < S || vt_ld % 64 != 0)))
+    return fail(CDX_EINVAL, "%s: vt_ld=%lld must be 0 or a multiple of 64 that is >= S", name, (long long)vt_ld);
   if (M == 0) return CDX_OK;
   if (pos0 + S > n_pos)
     return fail(CDX_EINVAL, "%s: cos/sin table has %lld positions, needs %lld", name, (long long)n_pos,
@@ -221,6 +223,7 @@ extern "C" int cdx_mu_qkv_rope_fwd(const uint16_t* x, int64_t ldx, const uint16_
   p.qk.q_out = q_out;
   p.qk.k_out = k_out;
   p.qk.v_out = v_out;
+  p.qk.vt_ld = vt_ld;
   if (cdiv(M, kBM) > INT32_MAX) return fail(CDX_EUNSUPPORTED, "%s: M too large", name);
   p.mt_count = (int32_t)cdiv(M, kBM);
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);

@@ -187,6 +187,10 @@ int cdx_mu_qkv_fwd(const uint16_t* x_dev, int64_t ldx, const uint16_t* mu_dev, i
  *            n_pos >= pos0 + S positions (pos0 = tokens already in the KV cache).
  * q_norm_w / k_norm_w ([hd] bf16) both NULL: no QK norm.  hd must be 32, 64 or 128
  * and H a multiple of 64.  mu / ldmu / w_pack / ldw as in cdx_mu_qkv_fwd.
+ * vt_ld == 0: v_out is [B, nkv, S, hd].  vt_ld > 0 (a multiple of 64, >= S): v_out is
+ * V transposed for cdx_attention_fwd, [B, nkv, hd, vt_ld], token s of a sequence at
+ * column 16*(s/16) + 4*sigma((s/4)%4) + s%4 with sigma = (0 2 1 3); the columns of
+ * positions >= S are not written (cdx_attention_fwd needs them finite: clear them).
  *
  * Replaces: core/attention.py:120-155 (cat + three F.linear, head split, q_norm /
  * k_norm, rotary tables and apply_rotary_pos_emb), core/rotary.py:57-86.
@@ -196,7 +200,26 @@ int cdx_mu_qkv_rope_fwd(const uint16_t* x_dev, int64_t ldx, const uint16_t* mu_d
                         int32_t nq, int32_t nkv, int32_t hd, const uint16_t* q_norm_w_dev,
                         const uint16_t* k_norm_w_dev, float eps, const float* cos_sin_dev,
                         int64_t n_pos, int64_t pos0, uint16_t* q_out_dev, uint16_t* k_out_dev,
-                        uint16_t* v_out_dev, void* stream);
+                        uint16_t* v_out_dev, int64_t vt_ld, void* stream);
+
+/*
+ * Causal GQA attention over the fused projection's outputs:
+ *   out[b, s, h*hd : (h+1)*hd] = sum_{n <= s} softmax_n(scale * q[b,h,s] . k[b,g,n]) v[b,g,n]
+ * with g = h / (nq / nkv) (query heads share key/value heads in groups), the causal
+ * mask top-left aligned (key n visible to query s iff n <= s) and fp32 softmax.
+ *   q   [B, nq, S, hd] bf16;  k [B, nkv, S, hd] bf16
+ *   vt  V transposed, [B, nkv, hd, vt_ld] bf16, token n at column
+ *       16*(n/16) + 4*sigma((n/4)%4) + n%4, sigma = (0 2 1 3); vt_ld a multiple of 64
+ *       >= S; the columns of positions n >= S (masked keys) must hold finite values
+ *   out [B, S, nq * hd] bf16 (heads merged, the layout o_proj consumes)
+ * hd must be 32, 64 or 128 and nkv must divide nq.
+ *
+ * Replaces: core/attention.py:163-181 (repeat_interleave of K and V, SDPA with
+ * is_causal=True, transpose + merge of the heads).
+ */
+int cdx_attention_fwd(const uint16_t* q_dev, const uint16_t* k_dev, const uint16_t* vt_dev, int64_t B,
+                      int64_t S, int32_t nq, int32_t nkv, int32_t hd, int64_t vt_ld, float scale,
+                      uint16_t* out_dev, void* stream);
 
 #ifdef __cplusplus
 }

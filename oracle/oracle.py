@@ -19,6 +19,7 @@ What it restates (reference file:line it follows):
   ``token_routed_mlp`` core/token_routed_mlp.py:142-178
   ``grouped_gemm``     cuda/triton_token_routed.py:64-86
   ``attention``        core/attention.py:115-181, core/rotary.py:30-86
+  ``causal_attention`` core/attention.py:162-181 (the attention core)
   ``forward``          models/modeling.py:176-206, core/layer.py:54-61,141-190
 
 How each function is pinned (independently of its own formula) is listed in the
@@ -245,15 +246,24 @@ def attention(x, mu, sd: Dict[str, torch.Tensor], prefix: str, cfg: dict):
     cos, sin = rope_tables(g("rotary_emb.inv_freq"), S)
     q = q * cos + _rotate_half(q) * sin
     k = k * cos + _rotate_half(k) * sin
-    rep = nq // nkv
+    o = causal_attention(q, k, v)
+    return o @ _f32(g("o_proj.weight")).t()
+
+
+def causal_attention(q, k, v):
+    """softmax(q k^T / sqrt(D), top-left causal) v with key/value heads repeated over
+    query-head groups, merged to [B, S, nq * D]; attention.py:162-181 (SDPA with
+    is_causal=True, then transpose + view).  q [B, nq, S, D], k/v [B, nkv, Skv, D]."""
+    q, k, v = _f32(q), _f32(k), _f32(v)
+    B, nq, S, D = q.shape
+    rep = nq // k.shape[1]
     k = k.repeat_interleave(rep, dim=1)
     v = v.repeat_interleave(rep, dim=1)
     scores = (q @ k.transpose(-2, -1)) / math.sqrt(D)
-    causal = torch.ones(S, S, dtype=torch.bool).triu(1)
+    causal = torch.ones(S, k.shape[2], dtype=torch.bool).triu(1)
     scores = scores.masked_fill(causal, float("-inf"))
     o = torch.softmax(scores, dim=-1) @ v
-    o = o.transpose(1, 2).reshape(B, S, nq * D)
-    return o @ _f32(g("o_proj.weight")).t()
+    return o.transpose(1, 2).reshape(B, S, nq * D)
 
 
 def forward(sd: Dict[str, torch.Tensor], cfg: dict, input_ids: torch.Tensor) -> torch.Tensor:

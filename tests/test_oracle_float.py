@@ -121,3 +121,27 @@ def test_grouped_gemm_brute_force(oracle):
     for r in range(16):
         e = int(np.searchsorted(offs, r, side="right") - 1)
         torch.testing.assert_close(out[r], a[r] @ w[e], rtol=1e-5, atol=1e-5)
+
+
+@pytest.mark.parametrize("nq,nkv,S,D", [(4, 2, 37, 16), (6, 6, 20, 8), (8, 2, 64, 32)])
+def test_causal_attention_vs_library_sdpa(oracle, nq, nkv, S, D):
+    """The attention core against torch's scaled_dot_product_attention(is_causal=True)
+    (a library routine) on repeated K/V heads, and the causal property: the output for
+    query s does not change when keys/values after s are perturbed."""
+    g = torch.Generator().manual_seed(S)
+    q = torch.randn(2, nq, S, D, generator=g, dtype=torch.float64)
+    k = torch.randn(2, nkv, S, D, generator=g, dtype=torch.float64)
+    v = torch.randn(2, nkv, S, D, generator=g, dtype=torch.float64)
+    out = oracle.causal_attention(q, k, v)
+    rep = nq // nkv
+    lib = torch.nn.functional.scaled_dot_product_attention(
+        q, k.repeat_interleave(rep, 1), v.repeat_interleave(rep, 1), is_causal=True)
+    lib = lib.transpose(1, 2).reshape(2, S, nq * D).float()
+    assert torch.allclose(out, lib, atol=1e-5, rtol=1e-5)
+    s = S // 2
+    k2, v2 = k.clone(), v.clone()
+    k2[:, :, s + 1:] += 3.0
+    v2[:, :, s + 1:] -= 5.0
+    out2 = oracle.causal_attention(q, k2, v2)
+    assert torch.allclose(out[:, : s + 1], out2[:, : s + 1], atol=1e-6)
+    assert not torch.allclose(out[:, s + 1:], out2[:, s + 1:])
