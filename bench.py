@@ -82,6 +82,8 @@ def work_of(name: str, s: dict):
         return float(rows * (4 if s["store_residual"] else 3) + 2 * s["H"]), "byte"
     if name == "rmsnorm":
         return float(2 * s["T"] * s["H"] * 2 + 2 * s["H"]), "byte"
+    if name == "mu_guidance":
+        return 2.0 * s["T"] * s["H"] * s["H"], "flop"
     if name == "attention":
         # causal: query s sees s + 1 keys; QK^T and PV are 2 * D FLOP per (query, key) each
         S = s["S"]

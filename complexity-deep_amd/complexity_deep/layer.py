@@ -1,7 +1,7 @@
 """Decoder block and mu guidance; interfaces of core/layer.py:28-190.
 
 ``TransformerBlock.forward`` keeps the reference signature and returns
-(hidden_states, new_kv, mu).  Inside, the residual add before the MLP's norm is the
+(hidden_states, new_kv, mu) with mu unclamped, as the reference does.  Inside, the residual add before the MLP's norm is the
 fused add+RMSNorm kernel.  ``ComplexityModel`` drives the blocks through
 ``forward_fused``, which also fuses the add after the MLP with the *next* norm (the
 next layer's input norm or the final norm) and reuses one routing plan for all
@@ -10,20 +10,44 @@ layers.
 
 from __future__ import annotations
 
+import math
 from typing import Optional, Tuple
 
 import torch
 import torch.nn as nn
 import torch.nn.functional as F
 
+from . import _native as nat
+from ._grad import forward_only
 from .attention import ComplexityAttention
 from .mlp import SwiGLU
 from .normalization import RMSNorm, add_rms_norm
 from .token_routed_mlp import RoutePlan, TokenRoutedMLP
 
 
+def mu_guidance(h: torch.Tensor, w: torch.Tensor, bias: torch.Tensor, lo: float = -math.inf,
+                hi: float = math.inf) -> torch.Tensor:
+    """clamp(h @ w^T + bias, lo, hi) through cdx_mu_guidance_fwd (fp32 accumulate, one
+    rounding).  h [..., H] bf16, w [H, H] bf16, bias [H] fp32."""
+    nat.require_device(h, w, what="mu_guidance")
+    H = h.shape[-1]
+    h2 = h.reshape(-1, H)
+    h2 = h2 if h2.is_contiguous() else h2.contiguous()
+    w = w if w.is_contiguous() else w.contiguous()
+    out = torch.empty(h.shape, dtype=h.dtype, device=h.device)
+    with nat.launch_region("mu_guidance", h.device, T=h2.shape[0], H=H):
+        nat.check(nat.lib().cdx_mu_guidance_fwd(h2.data_ptr(), h2.shape[0], H, w.data_ptr(), bias.data_ptr(),
+                                                float(lo), float(hi), out.data_ptr(), nat.stream_of(h)),
+                  "cdx_mu_guidance_fwd")
+    return out
+
+
 class MuGuidance(nn.Module):
-    """mu = clamp(mu_param, mu_min, mu_max) + mu_proj(h); core/layer.py:28-61."""
+    """mu = clamp(mu_param, mu_min, mu_max) + mu_proj(h); core/layer.py:28-61.
+
+    Runs as one kernel (cdx_mu_guidance_fwd): the mu_proj GEMM with the clamped
+    parameter added in its epilogue; ``fused(h, lo, hi)`` also applies the clamp the
+    model puts on mu between layers (models/modeling.py:199-200)."""
 
     def __init__(self, hidden_size: int, mu_min: float = 0.0, mu_max: float = 2.0):
         super().__init__()
@@ -32,9 +56,23 @@ class MuGuidance(nn.Module):
         self.mu = nn.Parameter(torch.full((hidden_size,), (mu_min + mu_max) / 2))
         self.mu_proj = nn.Linear(hidden_size, hidden_size, bias=False)
         nn.init.zeros_(self.mu_proj.weight)
+        self._bias_key = None
+        self._bias = None
+
+    def _clamped_mu(self) -> torch.Tensor:
+        key = (self.mu.data_ptr(), self.mu._version, self.mu.device)
+        if key != self._bias_key:
+            with torch.no_grad():
+                self._bias = torch.clamp(self.mu.float(), self.mu_min, self.mu_max).contiguous()
+            self._bias_key = key
+        return self._bias
+
+    def fused(self, hidden_states: torch.Tensor, lo: float = -math.inf, hi: float = math.inf) -> torch.Tensor:
+        forward_only("MuGuidance", hidden_states, *self.parameters())
+        return mu_guidance(hidden_states, self.mu_proj.weight, self._clamped_mu(), lo, hi)
 
     def forward(self, hidden_states: torch.Tensor) -> torch.Tensor:
-        return torch.clamp(self.mu, self.mu_min, self.mu_max) + F.linear(hidden_states, self.mu_proj.weight)
+        return self.fused(hidden_states)
 
 
 class TransformerBlock(nn.Module):
@@ -91,8 +129,9 @@ class TransformerBlock(nn.Module):
         """One block given h (updated in place) and normed = input_layernorm(h).
 
         Returns (h, next_norm(h_out), new_kv, mu) where the residual add after the MLP
-        is fused with ``next_norm``.  ``want_mu=False`` skips mu for the last layer,
-        whose mu the reference computes and then discards (modeling.py:199-200)."""
+        is fused with ``next_norm`` and mu is already clamped to [-2, 2], the model's
+        clamp between layers (modeling.py:199-200).  ``want_mu=False`` skips mu for the
+        last layer, whose mu the reference computes and then discards."""
         attn_out, new_kv = self.self_attn(normed, attention_mask=attention_mask,
                                           past_key_value=past_key_value, use_cache=use_cache,
                                           mu_prev=mu_prev)
@@ -100,5 +139,5 @@ class TransformerBlock(nn.Module):
         normed, _ = add_rms_norm(attn_out, h, ln.weight, ln.eps, residual_out=h)
         mlp_out = self._mlp(normed, token_ids, route)
         normed, _ = add_rms_norm(mlp_out, h, next_norm.weight, next_norm.eps, residual_out=h)
-        mu = self.mu_guidance(h) if (want_mu and self.mu_guidance is not None) else None
+        mu = self.mu_guidance.fused(h, -2.0, 2.0) if (want_mu and self.mu_guidance is not None) else None
         return h, normed, new_kv, mu

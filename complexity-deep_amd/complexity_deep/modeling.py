@@ -12,8 +12,12 @@ The forward (modeling.py:155-219) runs the hot path on the gfx950 kernels:
   * a plain RMSNorm for layer 0's input, then every residual add fused with the
     norm that follows it (2L fused add+RMSNorm calls, the last one being the final
     norm);
+  * the mu-QKV projection carries QK-norm and RoPE in its epilogue and feeds the
+    causal GQA attention kernel (no mask, no KV cache);
+  * mu guidance is one kernel that also applies the [-2, 2] clamp between layers;
   * the last layer's mu, which the reference computes and discards, is skipped.
-Embedding, attention core, o_proj, mu_proj and lm_head run as PyTorch-ROCm ops.
+Embedding, o_proj and lm_head run as PyTorch-ROCm ops, as does attention with a
+mask or a KV cache (generation).
 """
 
 from __future__ import annotations
@@ -224,7 +228,7 @@ class ComplexityModel(nn.Module):
                 use_cache=use_cache, token_ids=input_ids, mu_prev=mu_prev, route=plans[i],
                 want_mu=not last)
             if mu is not None:
-                mu_prev = torch.clamp(mu, -2.0, 2.0)
+                mu_prev = mu  # clamped to [-2, 2] inside the mu-guidance kernel
             if use_cache:
                 new_kvs.append(new_kv)
         logits = self.lm_head(normed)

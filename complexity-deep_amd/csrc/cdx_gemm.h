@@ -7,7 +7,7 @@
 // owning a 128 x 128 sub-tile made of 4 x 4 blocks of 32 x 32 computed with
 // v_mfma_f32_32x32x16_bf16 (256 fp32 accumulators per lane, held in AGPRs).
 //
-// Global -> LDS: direct-to-LDS loads (global_load_lds_dwordx4).  One wave instruction
+// Global -> LDS: direct-to-LDS buffer loads (buffer_load_dwordx4 ... lds).  One wave instruction
 // writes 64 x 16 bytes = 1 KB of LDS contiguously (lane i at base + 16 i), i.e. eight
 // 128-byte tile rows.  The LDS tile is row-major, 128 bytes per row (64 bf16 of K),
 // with 16-byte chunk c of row r stored at chunk position c ^ (r & 7); the swizzle is
@@ -41,7 +41,7 @@
 namespace cdx {
 
 enum class ALoad { kDense, kConcat, kGather };
-enum class Epi { kStore, kSwiGLU, kScatter, kQKRope };
+enum class Epi { kStore, kSwiGLU, kScatter, kQKRope, kBiasClamp };
 
 // Parameters of the kQKRope epilogue (mu-QKV with QK RMSNorm and RoPE fused): the
 // packed [M, (nq + 2 nkv) * HD] projection is never stored; q, k and v go straight
@@ -98,6 +98,9 @@ struct GemmParams {
   int32_t mt_count;  // number of M tiles (upper bound for grouped GEMMs)
   int32_t nt_count;
   QKRopeParams qk;  // kQKRope epilogue only
+  // kBiasClamp epilogue: c = clamp(acc + bias[n], lo, hi)
+  const float* bias;  // [N] fp32
+  float lo, hi;
 };
 
 constexpr int kBM = 256;
@@ -133,6 +136,21 @@ __device__ __forceinline__ float silu_f32(float g) { return g / (1.0f + __expf(-
 // s_waitcnt immediate (gfx9 layout: vmcnt bits 3:0 and 15:14, expcnt 6:4, lgkmcnt 11:8).
 constexpr int waitcnt_imm(int vm, int lgkm) {
   return (vm & 15) | ((vm >> 4) << 14) | (7 << 4) | ((lgkm & 15) << 8);
+}
+
+// Raw buffer descriptor over [base, base + 4 GB): stride 0, 32-bit data format
+// (descriptor word 3 = 0x00020000, the gfx9 layout), so the offset range check passes
+// every 32-bit offset.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)0xFFFFFFFFu, 0x00020000);
+}
+
+// 16 bytes per lane from buffer offset voff + soff straight into LDS at
+// lds_block + 16 * lane (buffer_load_dwordx4 ... lds).
+__device__ __forceinline__ void buf_dma16(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff,
+                                          uint8_t* lds_block) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void*)lds_block, 16, voff, soff,
+                                           0, 0);
 }
 
 // 16 bytes from global memory straight into LDS at lds_block + 16 * lane.
@@ -211,20 +229,30 @@ __global__ __launch_bounds__(kGemmThreads, Cfg::MINB) void gemm_nt_kernel(const 
   // side: lane i of a DMA instruction fills position i % CPR of row i / CPR of its
   // 1 KB block and therefore fetches global chunk (i % CPR) ^ ((row / RPL) % CPR).
   // Wave w fills rows [64 w, 64 w + 64) of both operands.
+  // The DMA goes through buffer descriptors: each lane's byte offset inside its
+  // operand is fixed for the whole K loop and the K position travels in the
+  // instruction's scalar offset, so a DMA costs no vector instruction.  Dense and
+  // concat A and B offsets are relative to the tile's first row (< 4 GB for any
+  // practical leading dimension); gathered A offsets are relative to the matrix,
+  // which the host bounds to 4 GB.
   const int dr = lane / CPR;
-  const uint16_t* a_src[LD_A];
-  const uint16_t* a2_src[LD_A];
-  const uint16_t* b_src[LD_B];
   const uint16_t* bexp = p.b + (int64_t)e * p.b_estride;
+  const __amdgpu_buffer_rsrc_t rs_a = make_rsrc(AL == ALoad::kGather ? p.a : p.a + m0 * p.lda);
+  const __amdgpu_buffer_rsrc_t rs_a2 = make_rsrc(AL == ALoad::kConcat ? p.a2 + m0 * p.lda2 : p.a);
+  const __amdgpu_buffer_rsrc_t rs_b = make_rsrc(bexp + (int64_t)n0 * p.ldb);
+  uint32_t a_off[LD_A], a2_off[LD_A], b_off[LD_B];
 #pragma unroll
   for (int j = 0; j < LD_A; ++j) {
     const int r = wave * (kBM / 4) + j * ROWS_PER_DMA + dr;
     const int dchunk = (lane % CPR) ^ ((r / RPL) % CPR);
     int64_t gm = m0 + r;
     gm = gm < m_end ? gm : m_end - 1;  // rows past the segment are loaded but never stored
-    const int64_t row = (AL == ALoad::kGather) ? (int64_t)p.perm[gm] : gm;
-    a_src[j] = p.a + row * p.lda + dchunk * 8;
-    if (AL == ALoad::kConcat) a2_src[j] = p.a2 + row * p.lda2 + dchunk * 8;
+    if (AL == ALoad::kGather) {
+      a_off[j] = (uint32_t)(((int64_t)p.perm[gm] * p.lda + dchunk * 8) * 2);
+    } else {
+      a_off[j] = (uint32_t)(((gm - m0) * p.lda + dchunk * 8) * 2);
+    }
+    a2_off[j] = AL == ALoad::kConcat ? (uint32_t)(((gm - m0) * p.lda2 + dchunk * 8) * 2) : 0u;
   }
 #pragma unroll
   for (int j = 0; j < LD_B; ++j) {
@@ -232,7 +260,7 @@ __global__ __launch_bounds__(kGemmThreads, Cfg::MINB) void gemm_nt_kernel(const 
     const int dchunk = (lane % CPR) ^ ((r / RPL) % CPR);
     int n = n0 + r;
     n = n < p.N ? n : p.N - 1;
-    b_src[j] = bexp + (int64_t)n * p.ldb + dchunk * 8;
+    b_off[j] = (uint32_t)(((int64_t)(n - n0) * p.ldb + dchunk * 8) * 2);
   }
   const int a_dma_off = wave * (kBM / 4) * ROW_BYTES;  // this wave's first DMA block in A
   const int b_dma_off = A_TILE_BYTES + wave * (kBN / 4) * ROW_BYTES;
@@ -240,16 +268,15 @@ __global__ __launch_bounds__(kGemmThreads, Cfg::MINB) void gemm_nt_kernel(const 
   // One DMA instruction of step kt into `stage`: d < LD_A covers A rows, then B.
   auto dma1 = [&](int kt, int stage, int d) __attribute__((always_inline)) {
     const int k0 = kt * kBK;
+    uint8_t* dst = lds + stage * STAGE_BYTES;
     if (d < LD_A) {
-      const uint16_t* src;
-      if (AL == ALoad::kConcat) {
-        src = (k0 < p.k_split) ? a_src[d] + k0 : a2_src[d] + (k0 - p.k_split);
+      if (AL == ALoad::kConcat && k0 >= p.k_split) {
+        buf_dma16(rs_a2, a2_off[d], (uint32_t)(k0 - p.k_split) * 2, dst + a_dma_off + d * 1024);
       } else {
-        src = a_src[d] + k0;
+        buf_dma16(rs_a, a_off[d], (uint32_t)k0 * 2, dst + a_dma_off + d * 1024);
       }
-      dma16(src, lds + stage * STAGE_BYTES + a_dma_off + d * 1024);
     } else {
-      dma16(b_src[d - LD_A] + k0, lds + stage * STAGE_BYTES + b_dma_off + (d - LD_A) * 1024);
+      buf_dma16(rs_b, b_off[d - LD_A], (uint32_t)k0 * 2, dst + b_dma_off + (d - LD_A) * 1024);
     }
   };
   auto issue = [&](int kt, int stage) __attribute__((always_inline)) {
@@ -374,7 +401,29 @@ __global__ __launch_bounds__(kGemmThreads, Cfg::MINB) void gemm_nt_kernel(const 
   kstep(kt, stage, 0, false, false, true);
 
   // ---- epilogue --------------------------------------------------------------
+  // Results are staged through LDS: each wave writes its WM rows in the MFMA output
+  // layout (8 bytes per lane and 4-column group) into its own region, rows of
+  // OUT_ROWB bytes with 16-byte chunk c of row r at position c ^ (r % OUT_CH), then
+  // reads them back 16 bytes per lane along the rows and stores whole row segments.
+  // A store instruction then covers a few contiguous row pieces (1 KB in total)
+  // instead of 8 bytes in each of 32 rows, which costs the L1 and L2 four times
+  // fewer accesses.  Transposed V (kQKRope with vt_ld > 0) is stored directly.
   const int hi = lane >> 5;
+  constexpr int OUT_COLS = EP == Epi::kSwiGLU ? WN / 2 : WN;  // output columns per wave
+  constexpr int OUT_ROWB = OUT_COLS * 2;
+  constexpr int OUT_CH = OUT_ROWB / 16;
+  constexpr int RPI = 64 / OUT_CH;  // rows per store instruction
+  static_assert(4 * WM * OUT_ROWB <= kStages * STAGE_BYTES, "epilogue staging must fit the LDS");
+  __syncthreads();  // every wave is done with the pipeline's LDS stages
+  uint8_t* ep = lds + wave * (WM * OUT_ROWB);
+  auto stage4 = [&](int r, int col, float y0, float y1, float y2, float y3) __attribute__((always_inline)) {
+    uint2 o;
+    o.x = pack_bf16x2(y0, y1);
+    o.y = pack_bf16x2(y2, y3);
+    const int ch = (col >> 3) ^ (r % OUT_CH);
+    *reinterpret_cast<uint2*>(ep + r * OUT_ROWB + ch * 16 + ((col >> 2) & 1) * 8) = o;
+  };
+
   if constexpr (EP == Epi::kQKRope) {
     // Head-wise epilogue.  A wave's WN columns hold WN / HD whole heads; for row m
     // a lane holds half of a head's HD values (its partner lane l ^ 32 the rest),
@@ -390,12 +439,11 @@ __global__ __launch_bounds__(kGemmThreads, Cfg::MINB) void gemm_nt_kernel(const 
       if (c0 >= p.N) continue;
       const int kind = c0 < qd ? 0 : (c0 < qd + kvd ? 1 : 2);  // q, k, v
       const int head = kind == 0 ? c0 / HD : (kind == 1 ? (c0 - qd) / HD : (c0 - qd - kvd) / HD);
-      const int nheads = kind == 0 ? q.nq : q.nkv;
-      uint16_t* obase = kind == 0 ? q.q_out : (kind == 1 ? q.k_out : q.v_out);
       const uint16_t* nw = kind == 0 ? q.q_norm_w : (kind == 1 ? q.k_norm_w : nullptr);
 #pragma unroll
       for (int mi = 0; mi < MI; ++mi) {
-        const int64_t gm = m0 + wm * WM + mi * 32 + (lane & 31);
+        const int r = mi * 32 + (lane & 31);
+        const int64_t gm = m0 + wm * WM + r;
         float x[BPH][16];
 #pragma unroll
         for (int nb = 0; nb < BPH; ++nb)
@@ -409,7 +457,7 @@ __global__ __launch_bounds__(kGemmThreads, Cfg::MINB) void gemm_nt_kernel(const 
 #pragma unroll
             for (int v = 0; v < 16; ++v) ss += x[nb][v] * x[nb][v];
           ss += __shfl_xor(ss, 32, 64);
-          const float r = rsqrtf(ss / (float)HD + q.eps);
+          const float rs = rsqrtf(ss / (float)HD + q.eps);
 #pragma unroll
           for (int nb = 0; nb < BPH; ++nb)
 #pragma unroll
@@ -418,22 +466,15 @@ __global__ __launch_bounds__(kGemmThreads, Cfg::MINB) void gemm_nt_kernel(const 
               const float w4[4] = {__uint_as_float(wv.x << 16), __uint_as_float(wv.x & 0xffff0000u),
                                    __uint_as_float(wv.y << 16), __uint_as_float(wv.y & 0xffff0000u)};
 #pragma unroll
-              for (int j = 0; j < 4; ++j) x[nb][4 * g + j] = w4[j] * (x[nb][4 * g + j] * r);
+              for (int j = 0; j < 4; ++j) x[nb][4 * g + j] = w4[j] * (x[nb][4 * g + j] * rs);
             }
         }
         if (gm >= m_end) continue;
-        const int64_t b = gm / q.S, s = gm - b * q.S;
-        uint16_t* orow = obase + (((b * nheads + head) * q.S) + s) * HD;
-        auto store4 = [&](int c, float y0, float y1, float y2, float y3) __attribute__((always_inline)) {
-          uint2 o;
-          o.x = pack_bf16x2(y0, y1);
-          o.y = pack_bf16x2(y2, y3);
-          *reinterpret_cast<uint2*>(orow + c) = o;
-        };
         if (kind == 2) {
           if (q.vt_ld > 0) {
             // V^T: column vt_col(s) of rows d; 32 consecutive tokens per half wave.
-            uint16_t* vt = q.v_out + ((b * nheads + head) * HD) * q.vt_ld + vt_col(s);
+            const int64_t b = gm / q.S, s = gm - b * q.S;
+            uint16_t* vt = q.v_out + ((b * q.nkv + head) * HD) * q.vt_ld + vt_col(s);
 #pragma unroll
             for (int nb = 0; nb < BPH; ++nb)
 #pragma unroll
@@ -447,11 +488,13 @@ __global__ __launch_bounds__(kGemmThreads, Cfg::MINB) void gemm_nt_kernel(const 
           for (int nb = 0; nb < BPH; ++nb)
 #pragma unroll
             for (int g = 0; g < 4; ++g)
-              store4(nb * 32 + 8 * g + 4 * hi, x[nb][4 * g], x[nb][4 * g + 1], x[nb][4 * g + 2], x[nb][4 * g + 3]);
+              stage4(r, hb * HD + nb * 32 + 8 * g + 4 * hi, x[nb][4 * g], x[nb][4 * g + 1], x[nb][4 * g + 2],
+                     x[nb][4 * g + 3]);
           continue;
         }
         // RoPE on each pair (c, c + HALF), c < HALF, sharing the angle of index c:
         //   y[c] = x[c] cos - x[c + HALF] sin,  y[c + HALF] = x[c + HALF] cos + x[c] sin.
+        const int64_t s = gm % q.S;
         const float2* cs = reinterpret_cast<const float2*>(q.cos_sin) + (q.pos0 + s) * HALF;
         constexpr int NB_LO = HD >= 64 ? BPH / 2 : 1;  // 32-column blocks holding first-half columns
         constexpr int G_LO = HD >= 64 ? 4 : 2;         // groups of 4 slots per block in the first half
@@ -472,57 +515,88 @@ __global__ __launch_bounds__(kGemmThreads, Cfg::MINB) void gemm_nt_kernel(const 
               lo[j] = a * cv[j] - bq * sv[j];
               up[j] = bq * cv[j] + a * sv[j];
             }
-            store4(c, lo[0], lo[1], lo[2], lo[3]);
-            store4(c + HALF, up[0], up[1], up[2], up[3]);
+            stage4(r, hb * HD + c, lo[0], lo[1], lo[2], lo[3]);
+            stage4(r, hb * HD + c + HALF, up[0], up[1], up[2], up[3]);
           }
       }
     }
-    return;
-  }
+  } else if constexpr (EP == Epi::kSwiGLU) {
+    // Packed B rows come in groups of 64: 32 gate rows then the matching 32 up rows;
+    // the wave's output columns are (ni / 2) * 32 + 8 g + 4 hi.
 #pragma unroll
-  for (int mi = 0; mi < MI; ++mi) {
-    const int64_t gm = m0 + wm * WM + mi * 32 + (lane & 31);
-    if (gm >= m_end) continue;
-    if constexpr (EP == Epi::kSwiGLU) {
-      // Packed B rows come in groups of 64: 32 gate rows then the matching 32 up rows.
-      uint16_t* crow = p.c + gm * p.ldc;
+    for (int mi = 0; mi < MI; ++mi) {
+      const int r = mi * 32 + (lane & 31);
 #pragma unroll
-      for (int ni = 0; ni < NI; ni += 2) {
-        const int nb = n0 + wn * WN + ni * 32;  // multiple of 64
-        if (nb >= p.N) continue;
-        const int colb = (nb >> 6) * 32;
+      for (int ni = 0; ni < NI; ni += 2)
 #pragma unroll
         for (int g = 0; g < 4; ++g) {
           float a4[4];
 #pragma unroll
-          for (int j = 0; j < 4; ++j) {
-            const float gate = acc[mi][ni][4 * g + j];
-            const float up = acc[mi][ni + 1][4 * g + j];
-            a4[j] = silu_f32(gate) * up;
-          }
-          uint2 v;
-          v.x = pack_bf16x2(a4[0], a4[1]);
-          v.y = pack_bf16x2(a4[2], a4[3]);
-          *reinterpret_cast<uint2*>(crow + colb + 8 * g + 4 * hi) = v;
+          for (int j = 0; j < 4; ++j)
+            a4[j] = silu_f32(acc[mi][ni][4 * g + j]) * acc[mi][ni + 1][4 * g + j];
+          stage4(r, (ni >> 1) * 32 + 8 * g + 4 * hi, a4[0], a4[1], a4[2], a4[3]);
         }
-      }
-    } else {
-      const int64_t orow = (EP == Epi::kScatter) ? (int64_t)p.perm[gm] : gm;
-      uint16_t* crow = p.c + orow * p.ldc;
+    }
+  } else {
 #pragma unroll
-      for (int ni = 0; ni < NI; ++ni) {
+    for (int mi = 0; mi < MI; ++mi) {
+      const int r = mi * 32 + (lane & 31);
+#pragma unroll
+      for (int ni = 0; ni < NI; ++ni)
 #pragma unroll
         for (int g = 0; g < 4; ++g) {
-          const int n = n0 + wn * WN + ni * 32 + 8 * g + 4 * hi;
-          if (n < p.N) {
-            uint2 v;
-            v.x = pack_bf16x2(acc[mi][ni][4 * g + 0], acc[mi][ni][4 * g + 1]);
-            v.y = pack_bf16x2(acc[mi][ni][4 * g + 2], acc[mi][ni][4 * g + 3]);
-            *reinterpret_cast<uint2*>(crow + n) = v;
+          const int col = ni * 32 + 8 * g + 4 * hi;
+          float y[4] = {acc[mi][ni][4 * g + 0], acc[mi][ni][4 * g + 1], acc[mi][ni][4 * g + 2],
+                        acc[mi][ni][4 * g + 3]};
+          if constexpr (EP == Epi::kBiasClamp) {
+            const int n = n0 + wn * WN + col;
+            if (n < p.N) {
+              const float4 bv = *reinterpret_cast<const float4*>(p.bias + n);
+              const float bb[4] = {bv.x, bv.y, bv.z, bv.w};
+#pragma unroll
+              for (int j = 0; j < 4; ++j) y[j] = fminf(fmaxf(y[j] + bb[j], p.lo), p.hi);
+            }
           }
+          stage4(r, col, y[0], y[1], y[2], y[3]);
         }
-      }
     }
+  }
+
+  // Own LDS writes are complete before the reads (LDS operations of a wave execute
+  // in order; the wait also keeps the compiler from reordering them).
+  __builtin_amdgcn_s_waitcnt(waitcnt_imm(63, 0));
+  const int jc = lane % OUT_CH;  // this lane's chunk of a row
+#pragma unroll 4
+  for (int i = 0; i < WM / RPI; ++i) {
+    const int r = i * RPI + lane / OUT_CH;
+    const int64_t gm = m0 + wm * WM + r;
+    if (gm >= m_end) continue;
+    const uint4 v = *reinterpret_cast<const uint4*>(ep + r * OUT_ROWB + ((jc ^ (r % OUT_CH)) << 4));
+    const int col = jc * 8;  // first output column of the chunk within the wave
+    uint16_t* dst;
+    if constexpr (EP == Epi::kQKRope) {
+      const QKRopeParams& q = p.qk;
+      const int qd = q.nq * HD, kvd = q.nkv * HD;
+      const int c0 = n0 + wn * WN + (col / HD) * HD;
+      if (c0 >= p.N) continue;
+      const int kind = c0 < qd ? 0 : (c0 < qd + kvd ? 1 : 2);
+      if (kind == 2 && q.vt_ld > 0) continue;  // stored directly above
+      const int head = kind == 0 ? c0 / HD : (kind == 1 ? (c0 - qd) / HD : (c0 - qd - kvd) / HD);
+      const int nheads = kind == 0 ? q.nq : q.nkv;
+      uint16_t* obase = kind == 0 ? q.q_out : (kind == 1 ? q.k_out : q.v_out);
+      const int64_t b = gm / q.S, s = gm - b * q.S;
+      dst = obase + ((b * nheads + head) * q.S + s) * HD + (col % HD);
+    } else if constexpr (EP == Epi::kSwiGLU) {
+      const int n = (n0 + wn * WN) / 2 + col;
+      if (2 * n >= p.N) continue;
+      dst = p.c + gm * p.ldc + n;
+    } else {
+      const int n = n0 + wn * WN + col;
+      if (n >= p.N) continue;
+      const int64_t orow = EP == Epi::kScatter ? (int64_t)p.perm[gm] : gm;
+      dst = p.c + orow * p.ldc + n;
+    }
+    *reinterpret_cast<uint4*>(dst) = v;
   }
 }
 

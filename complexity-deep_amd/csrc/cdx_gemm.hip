@@ -5,6 +5,8 @@
 //   cdx_moe_swiglu_fwd   piece 1b: gather + gate/up + SwiGLU, then down + scatter,
 //                        with the shared expert folded into both passes
 //   cdx_grouped_gemm_fwd plain grouped GEMM over expert segments
+//   cdx_mu_guidance_fwd  mu = clamp(h @ W_mu^T + clamp(mu_param), lo, hi), the
+//                        producer of the next layer's mu operand
 #include "cdx_gemm.h"
 
 namespace cdx {
@@ -81,6 +83,8 @@ extern "C" int cdx_moe_swiglu_fwd(const uint16_t* x, int64_t T, int32_t H, int32
   if (T < 0 || T > INT32_MAX || H <= 0 || Ie <= 0 || E <= 0 || E > 64)
     return fail(CDX_EINVAL, "%s: bad shape T=%lld H=%d Ie=%d E=%d", name, (long long)T, H, Ie, E);
   if (H % 64 != 0) return fail(CDX_EUNSUPPORTED, "%s: H=%d must be a multiple of 64", name, H);
+  if (T * (int64_t)H * 2 > (int64_t)UINT32_MAX)
+    return fail(CDX_EUNSUPPORTED, "%s: x must fit 4 GB (T=%lld, H=%d)", name, (long long)T, H);
   if (T == 0) return CDX_OK;
   if (!x || !perm || !offsets || !w_gu || !w_down || !inter || !out)
     return fail(CDX_EINVAL, "%s: null pointer", name);
@@ -238,4 +242,36 @@ extern "C" int cdx_mu_qkv_rope_fwd(const uint16_t* x, int64_t ldx, const uint16_
       return mu ? launch<ALoad::kConcat, Epi::kQKRope, DefaultCfg, 128>(p, st, name)
                 : launch<ALoad::kDense, Epi::kQKRope, DefaultCfg, 128>(p, st, name);
   }
+}
+
+extern "C" int cdx_mu_guidance_fwd(const uint16_t* h, int64_t T, int32_t H, const uint16_t* w,
+                                   const float* bias, float lo, float hi, uint16_t* out, void* stream) {
+  using namespace cdx;
+  clear_error();
+  const char* name = "cdx_mu_guidance_fwd";
+  if (T < 0 || H <= 0) return fail(CDX_EINVAL, "%s: bad shape T=%lld H=%d", name, (long long)T, H);
+  if (H % 64 != 0) return fail(CDX_EUNSUPPORTED, "%s: H=%d must be a multiple of 64", name, H);
+  if (!(lo <= hi)) return fail(CDX_EINVAL, "%s: clamp range must satisfy lo <= hi", name);
+  if (T == 0) return CDX_OK;
+  if (!h || !w || !bias || !out) return fail(CDX_EINVAL, "%s: null pointer", name);
+  if (!aligned16(h) || !aligned16(w) || !aligned16(bias) || !aligned16(out))
+    return fail(CDX_EUNSUPPORTED, "%s: pointers must be 16-byte aligned", name);
+  GemmParams p{};
+  p.a = h;
+  p.lda = H;
+  p.k_split = H;
+  p.E = 1;
+  p.M = T;
+  p.b = w;
+  p.ldb = H;
+  p.N = H;
+  p.K = H;
+  p.c = out;
+  p.ldc = H;
+  p.bias = bias;
+  p.lo = lo;
+  p.hi = hi;
+  if (cdiv(T, kBM) > INT32_MAX) return fail(CDX_EUNSUPPORTED, "%s: T too large", name);
+  p.mt_count = (int32_t)cdiv(T, kBM);
+  return launch<ALoad::kDense, Epi::kBiasClamp>(p, reinterpret_cast<hipStream_t>(stream), name);
 }

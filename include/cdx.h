@@ -203,6 +203,20 @@ int cdx_mu_qkv_rope_fwd(const uint16_t* x_dev, int64_t ldx, const uint16_t* mu_d
                         uint16_t* v_out_dev, int64_t vt_ld, void* stream);
 
 /*
+ * mu guidance, the producer of the next layer's mu operand:
+ *   out[t, n] = clamp(sum_k h[t, k] w[n, k] + bias[n], lo, hi)
+ * h [T, H] bf16, w [H, H] bf16 (nn.Linear layout, [out, in]), bias [H] fp32, out [T, H]
+ * bf16; fp32 accumulation, one rounding.  The model passes bias = clamp(mu_param,
+ * mu_min, mu_max) and (lo, hi) = (-2, 2), its clamp of mu between layers; the module
+ * API passes (lo, hi) = (-inf, +inf).  H must be a multiple of 64.
+ *
+ * Replaces: core/layer.py:54-61 (MuGuidance.forward: clamp(mu) + mu_proj(h)) and
+ * models/modeling.py:199-200 (mu_prev = clamp(mu, -2, 2)).
+ */
+int cdx_mu_guidance_fwd(const uint16_t* h_dev, int64_t T, int32_t H, const uint16_t* w_dev,
+                        const float* bias_dev, float lo, float hi, uint16_t* out_dev, void* stream);
+
+/*
  * Causal GQA attention over the fused projection's outputs:
  *   out[b, s, h*hd : (h+1)*hd] = sum_{n <= s} softmax_n(scale * q[b,h,s] . k[b,g,n]) v[b,g,n]
  * with g = h / (nq / nkv) (query heads share key/value heads in groups), the causal
