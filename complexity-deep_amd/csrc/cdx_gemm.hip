@@ -18,6 +18,9 @@ int launch(GemmParams p, hipStream_t s, const char* name) {
   const int64_t nb = (int64_t)p.mt_count * p.nt_count;
   if (nb == 0) return CDX_OK;
   if (nb > INT32_MAX) return fail(CDX_EUNSUPPORTED, "%s: problem too large (%lld tiles)", name, (long long)nb);
+  // The kernel's K loop runs at least once and whole steps only.
+  if (p.K < Cfg::BK || p.K % Cfg::BK != 0)
+    return fail(CDX_EUNSUPPORTED, "%s: K=%d must be a positive multiple of %d", name, p.K, Cfg::BK);
   gemm_nt_kernel<Cfg, AL, EP, HD><<<dim3((unsigned)nb), dim3(kGemmThreads), 0, s>>>(p);
   return check_launch(name);
 }
