@@ -115,16 +115,21 @@ constexpr int kNumXcd = 8;
 // them in flight, MINB blocks resident per CU.  Stage s holds the A (256 x BK) and B
 // (BN x BK) tiles of one K step; the DMA of step k + STAGES is issued as soon as
 // stage k is consumed, so a load has STAGES - 1 K steps to land.
-template <int BN_, int BK_, int STAGES_, int MINB_>
+// DMA_EVERY / DMA_OFF place the refill DMA instructions of a K step behind MFMAs
+// DMA_OFF, DMA_OFF + DMA_EVERY, ... of its last sub-step (1, 0 = a burst behind the
+// first ones); READ_EVERY likewise spaces the fragment reads.
+template <int BN_, int BK_, int STAGES_, int MINB_, int DMA_EVERY_ = 1, int DMA_OFF_ = 0, int READ_EVERY_ = 1>
 struct GemmCfg {
   static constexpr int BN = BN_, BK = BK_, STAGES = STAGES_, MINB = MINB_;
+  static constexpr int DMA_EVERY = DMA_EVERY_, DMA_OFF = DMA_OFF_, READ_EVERY = READ_EVERY_;
+  static_assert(DMA_OFF < DMA_EVERY, "DMA slot offset must be below its spacing");
   static_assert(BN == 256 || BN == 128, "BN must be 128 or 256");
   static_assert(BK == 64, "BK must be 64 (two K32 sub-steps per stage)");
   static constexpr int STAGE_BYTES = (kBM + BN) * BK * 2;
   static_assert(STAGES >= 2 && STAGES * STAGE_BYTES * MINB <= 160 * 1024, "stages must fit 160 KB of LDS");
 };
 #ifndef CDX_GEMM_CFG
-#define CDX_GEMM_CFG 256, 64, 2, 1
+#define CDX_GEMM_CFG 256, 64, 2, 1, 4, 1, 1
 #endif
 using DefaultCfg = GemmCfg<CDX_GEMM_CFG>;
 
@@ -179,6 +184,7 @@ __global__ __launch_bounds__(kGemmThreads, Cfg::MINB) void gemm_nt_kernel(const 
   constexpr int LD_PER_STEP = LD_A + LD_B;
   constexpr int NSUB = kBK / 32;                    // K32 sub-steps per K step
   constexpr int NFRAG = MI + NI;                    // fragment reads per sub-step
+  constexpr int DMA_EVERY = Cfg::DMA_EVERY, DMA_OFF = Cfg::DMA_OFF, RD_EVERY = Cfg::READ_EVERY;
   static_assert(LD_B >= 1, "B tile too small for the DMA layout");
   static_assert(NSUB % 2 == 0, "fragment register sets alternate per sub-step: K step must hold an even count");
   static_assert(EP != Epi::kSwiGLU || (WN % 64) == 0, "SwiGLU needs gate/up pairs per wave");
@@ -346,7 +352,7 @@ __global__ __launch_bounds__(kGemmThreads, Cfg::MINB) void gemm_nt_kernel(const 
 #pragma unroll
     for (int i = 0; i < MI * NI; ++i) {
       mfma1(s & 1, i);
-      if (i < NFRAG) read1(stage, s + 1, (s + 1) & 1, i);
+      if (i % RD_EVERY == 0 && i / RD_EVERY < NFRAG) read1(stage, s + 1, (s + 1) & 1, i / RD_EVERY);
       __builtin_amdgcn_sched_barrier(0);
     }
   };
@@ -365,13 +371,13 @@ __global__ __launch_bounds__(kGemmThreads, Cfg::MINB) void gemm_nt_kernel(const 
 #pragma unroll
     for (int i = 0; i < MI * NI; ++i) {
       mfma1((NSUB - 1) & 1, i);
-      if (!last && i < LD_PER_STEP) dma1(kt + kStages, stage, i);
-      if (!last && i < NFRAG) read1(next_stage, 0, 0, i);
+      if (!last && i % DMA_EVERY == DMA_OFF && i / DMA_EVERY < LD_PER_STEP) dma1(kt + kStages, stage, i / DMA_EVERY);
+      if (!last && i % RD_EVERY == 0 && i / RD_EVERY < NFRAG) read1(next_stage, 0, 0, i / RD_EVERY);
       __builtin_amdgcn_sched_barrier(0);
     }
     if (!last) {
 #pragma unroll
-      for (int d = MI * NI; d < LD_PER_STEP; ++d) dma1(kt + kStages, stage, d);
+      for (int d = (MI * NI - DMA_OFF + DMA_EVERY - 1) / DMA_EVERY; d < LD_PER_STEP; ++d) dma1(kt + kStages, stage, d);
     }
     __builtin_amdgcn_sched_barrier(0);
   };
@@ -428,6 +434,31 @@ __global__ __launch_bounds__(kGemmThreads, Cfg::MINB) void gemm_nt_kernel(const 
     *reinterpret_cast<uint2*>(ep + r * OUT_ROWB + ch * 16 + ((col >> 2) & 1) * 8) = o;
   };
 
+  // kQKRope: token (b, s) of wave row r, from one division per wave for its first
+  // row (the host bounds S below 2^31 - 256, so s0 + r fits 32 bits).
+  int64_t tok_b0 = 0;
+  uint32_t tok_s0 = 0;
+  if constexpr (EP == Epi::kQKRope) {
+    const int64_t row_base = m0 + wm * WM;
+    tok_b0 = row_base / p.qk.S;
+    tok_s0 = (uint32_t)(row_base - tok_b0 * p.qk.S);
+  }
+  // kQKRope, V^T output: a wave whose columns are all V heads and whose WM rows are
+  // one run of tokens of one sequence starting at a multiple of 16 stages V^T through
+  // LDS (rows d of 256 bytes = its WM tokens in vt_col order) and stores whole row
+  // segments; other waves store V^T element by element.
+  bool vt_fast = false;
+  if constexpr (EP == Epi::kQKRope) {
+    vt_fast = p.qk.vt_ld > 0 && n0 + wn * WN >= (p.qk.nq + p.qk.nkv) * HD && (tok_s0 & 15) == 0 &&
+              (int64_t)tok_s0 + WM <= p.qk.S && m0 + wm * WM + WM <= m_end;
+  }
+  auto tok = [&](int r, int64_t& b, uint32_t& s) __attribute__((always_inline)) {
+    const uint32_t t = tok_s0 + (uint32_t)r, S32 = (uint32_t)p.qk.S;
+    const uint32_t w = t / S32;
+    s = t - w * S32;
+    b = tok_b0 + w;
+  };
+
   if constexpr (EP == Epi::kQKRope) {
     // Head-wise epilogue.  A wave's WN columns hold WN / HD whole heads of BPH
     // 16-column blocks; for row m a lane holds a quarter of the head's HD values
@@ -444,6 +475,32 @@ __global__ __launch_bounds__(kGemmThreads, Cfg::MINB) void gemm_nt_kernel(const 
       const int kind = c0 < qd ? 0 : (c0 < qd + kvd ? 1 : 2);  // q, k, v
       const int head = kind == 0 ? c0 / HD : (kind == 1 ? (c0 - qd) / HD : (c0 - qd - kvd) / HD);
       const uint16_t* nw = kind == 0 ? q.q_norm_w : (kind == 1 ? q.k_norm_w : nullptr);
+      const bool norm = kind != 2 && nw != nullptr;
+      // Norm weights of this lane's columns (the same for every row).
+      uint2 wpk[BPH];  // 4 bf16 each; one uniform branch around all the loads
+#pragma unroll
+      for (int nb = 0; nb < BPH; ++nb) wpk[nb] = make_uint2(0u, 0u);
+      if (norm) {
+#pragma unroll
+        for (int nb = 0; nb < BPH; ++nb) wpk[nb] = *reinterpret_cast<const uint2*>(nw + nb * 16 + 4 * q4);
+      }
+      // cos / sin of this lane's first-half columns for the rows of block mi, read at
+      // the top of the block so that the latency hides behind the norm arithmetic.
+      // Every row's s lies in [0, S), so the reads stay inside the table even past
+      // m_end.
+      float4 cs_cur[BPH / 2][2];
+      auto fetch_cs = [&](int mi, float4 (&dst)[BPH / 2][2]) __attribute__((always_inline)) {
+        int64_t b;
+        uint32_t s;
+        tok(mi * 16 + rl, b, s);
+        const float2* cs = reinterpret_cast<const float2*>(q.cos_sin) + (q.pos0 + s) * HALF;
+#pragma unroll
+        for (int nb = 0; nb < BPH / 2; ++nb) {
+          const int c = nb * 16 + 4 * q4;
+          dst[nb][0] = *reinterpret_cast<const float4*>(cs + c);
+          dst[nb][1] = *reinterpret_cast<const float4*>(cs + c + 2);
+        }
+      };
 #pragma unroll
       for (int mi = 0; mi < MI; ++mi) {
         __builtin_amdgcn_sched_barrier(0);  // one block of accumulators live at a time
@@ -454,30 +511,44 @@ __global__ __launch_bounds__(kGemmThreads, Cfg::MINB) void gemm_nt_kernel(const 
         for (int nb = 0; nb < BPH; ++nb)
 #pragma unroll
           for (int v = 0; v < 4; ++v) x[nb][v] = acc[mi][hb * BPH + nb][v];
-        if (kind != 2 && nw != nullptr) {
-          // RMSNorm over the head: this lane's quarter plus its three partners'.
-          float ss = 0.f;
-#pragma unroll
-          for (int nb = 0; nb < BPH; ++nb)
-#pragma unroll
-            for (int v = 0; v < 4; ++v) ss += x[nb][v] * x[nb][v];
-          ss += __shfl_xor(ss, 16, 64);
-          ss += __shfl_xor(ss, 32, 64);
-          const float rs = rsqrtf(ss / (float)HD + q.eps);
-#pragma unroll
-          for (int nb = 0; nb < BPH; ++nb) {
-            const uint2 wv = *reinterpret_cast<const uint2*>(nw + nb * 16 + 4 * q4);
-            const float w4[4] = {__uint_as_float(wv.x << 16), __uint_as_float(wv.x & 0xffff0000u),
-                                 __uint_as_float(wv.y << 16), __uint_as_float(wv.y & 0xffff0000u)};
-#pragma unroll
-            for (int j = 0; j < 4; ++j) x[nb][j] = w4[j] * (x[nb][j] * rs);
-          }
-        }
-        if (gm >= m_end) continue;
         if (kind == 2) {
+          if (vt_fast) {
+            // Quad transpose: lanes 4j + t (same q4) hold tokens 4j + t of dims
+            // 4 q4 + (0..3); afterwards lane 4j + t holds dim 4 q4 + t of tokens
+            // 4j + (0..3), as two packed bf16 pairs, in two exchange rounds (lane
+            // t ^ 1, then t ^ 2) over the quad.
+            const int t = lane & 3, j = (lane >> 2) & 3;
+            const bool odd = t & 1, upper = t & 2;
+#pragma unroll
+            for (int nb = 0; nb < BPH; ++nb) {
+              const uint32_t p0 = pack_bf16x2(x[nb][0], x[nb][1]), p1 = pack_bf16x2(x[nb][2], x[nb][3]);
+              // round 1: even lanes give dims 1, 3 and keep 0, 2; odd lanes the reverse.
+              const uint32_t give = __builtin_amdgcn_perm(p1, p0, odd ? 0x05040100u : 0x07060302u);
+              const uint32_t got = (uint32_t)__builtin_amdgcn_mov_dpp((int)give, 0xB1, 0xF, 0xF, true);
+              const uint32_t a0 = __builtin_amdgcn_perm(got, p0, odd ? 0x03020504u : 0x05040100u);
+              const uint32_t a1 = __builtin_amdgcn_perm(got, p1, odd ? 0x03020706u : 0x07060100u);
+              // round 2: lanes t < 2 give their second pair, t >= 2 their first.
+              const uint32_t give2 = upper ? a0 : a1;
+              const uint32_t got2 = (uint32_t)__builtin_amdgcn_mov_dpp((int)give2, 0x4E, 0xF, 0xF, true);
+              uint2 w;
+              w.x = upper ? got2 : a0;  // tokens 4j, 4j + 1
+              w.y = upper ? a1 : got2;  // tokens 4j + 2, 4j + 3
+              // Tokens r .. r + 3 (r = 16 mi + 4 j) sit at V^T positions
+              // 16 mi + 4 sigma(j) .. + 3; rows are 256 bytes with 16-byte chunk k
+              // at position k ^ (row % 16).
+              const int row = hb * HD + nb * 16 + 4 * q4 + t;
+              const int sj = j == 1 ? 2 : (j == 2 ? 1 : j);
+              const int chunk = 2 * mi + (sj >> 1);
+              *reinterpret_cast<uint2*>(ep + row * 256 + ((chunk ^ (row & 15)) << 4) + (sj & 1) * 8) = w;
+            }
+            continue;
+          }
+          if (gm >= m_end) continue;
           if (q.vt_ld > 0) {
             // V^T: column vt_col(s) of rows d; 16 consecutive tokens per quarter wave.
-            const int64_t b = gm / q.S, s = gm - b * q.S;
+            int64_t b;
+            uint32_t s;
+            tok(r, b, s);
             uint16_t* vt = q.v_out + ((b * q.nkv + head) * HD) * q.vt_ld + vt_col(s);
 #pragma unroll
             for (int nb = 0; nb < BPH; ++nb)
@@ -493,15 +564,32 @@ __global__ __launch_bounds__(kGemmThreads, Cfg::MINB) void gemm_nt_kernel(const 
             stage4(r, hb * HD + nb * 16 + 4 * q4, x[nb][0], x[nb][1], x[nb][2], x[nb][3]);
           continue;
         }
+        fetch_cs(mi, cs_cur);
+        if (norm) {
+          // RMSNorm over the head: this lane's quarter plus its three partners'.
+          float ss = 0.f;
+#pragma unroll
+          for (int nb = 0; nb < BPH; ++nb)
+#pragma unroll
+            for (int v = 0; v < 4; ++v) ss += x[nb][v] * x[nb][v];
+          ss += __shfl_xor(ss, 16, 64);
+          ss += __shfl_xor(ss, 32, 64);
+          const float rs = rsqrtf(ss / (float)HD + q.eps);
+#pragma unroll
+          for (int nb = 0; nb < BPH; ++nb) {
+            const float w4[4] = {__uint_as_float(wpk[nb].x << 16), __uint_as_float(wpk[nb].x & 0xffff0000u),
+                                 __uint_as_float(wpk[nb].y << 16), __uint_as_float(wpk[nb].y & 0xffff0000u)};
+#pragma unroll
+            for (int j = 0; j < 4; ++j) x[nb][j] = w4[j] * (x[nb][j] * rs);
+          }
+        }
+        if (gm >= m_end) continue;
         // RoPE on each pair (c, c + HALF), c < HALF, sharing the angle of index c:
         //   y[c] = x[c] cos - x[c + HALF] sin,  y[c + HALF] = x[c + HALF] cos + x[c] sin.
-        const int64_t s = gm % q.S;
-        const float2* cs = reinterpret_cast<const float2*>(q.cos_sin) + (q.pos0 + s) * HALF;
 #pragma unroll
         for (int nb = 0; nb < BPH / 2; ++nb) {
           const int c = nb * 16 + 4 * q4;  // first-half column, c % 4 == 0
-          const float4 t01 = *reinterpret_cast<const float4*>(cs + c);
-          const float4 t23 = *reinterpret_cast<const float4*>(cs + c + 2);
+          const float4 t01 = cs_cur[nb][0], t23 = cs_cur[nb][1];
           const float cv[4] = {t01.x, t01.z, t23.x, t23.z};
           const float sv[4] = {t01.y, t01.w, t23.y, t23.w};
           float lo[4], up[4];
@@ -523,7 +611,6 @@ __global__ __launch_bounds__(kGemmThreads, Cfg::MINB) void gemm_nt_kernel(const 
     // columns are 32 g + 16 (ni % 4) + 4 q4.
 #pragma unroll
     for (int mi = 0; mi < MI; ++mi) {
-      __builtin_amdgcn_sched_barrier(0);  // one block row of accumulators live at a time
       const int r = mi * 16 + rl;
 #pragma unroll
       for (int ni = 0; ni < NI; ni += 4)
@@ -538,7 +625,6 @@ __global__ __launch_bounds__(kGemmThreads, Cfg::MINB) void gemm_nt_kernel(const 
   } else {
 #pragma unroll
     for (int mi = 0; mi < MI; ++mi) {
-      __builtin_amdgcn_sched_barrier(0);  // one block row of accumulators live at a time
       const int r = mi * 16 + rl;
 #pragma unroll
       for (int ni = 0; ni < NI; ++ni) {
@@ -561,6 +647,25 @@ __global__ __launch_bounds__(kGemmThreads, Cfg::MINB) void gemm_nt_kernel(const 
   // Own LDS writes are complete before the reads (LDS operations of a wave execute
   // in order; the wait also keeps the compiler from reordering them).
   __builtin_amdgcn_s_waitcnt(waitcnt_imm(63, 0));
+  if constexpr (EP == Epi::kQKRope) {
+    if (vt_fast) {
+      // V^T rows: 16 lanes per 256-byte row, four rows per instruction.
+      static_assert(WM * 2 == 256, "a staged V^T row holds the wave's WM tokens in 256 bytes");
+      const QKRopeParams& q = p.qk;
+      const int k = lane & 15;
+#pragma unroll 4
+      for (int i = 0; i < WN / 4; ++i) {
+        const int row = i * 4 + (lane >> 4);
+        const int c0 = n0 + wn * WN + (row / HD) * HD;
+        if (c0 >= p.N) continue;
+        const int head = (c0 - (q.nq + q.nkv) * HD) / HD, d = row % HD;
+        const uint4 v = *reinterpret_cast<const uint4*>(ep + row * 256 + ((k ^ (row & 15)) << 4));
+        uint16_t* dst = q.v_out + ((tok_b0 * q.nkv + head) * HD + d) * q.vt_ld + tok_s0 + k * 8;
+        *reinterpret_cast<uint4*>(dst) = v;
+      }
+      return;
+    }
+  }
   const int jc = lane % OUT_CH;  // this lane's chunk of a row
 #pragma unroll 4
   for (int i = 0; i < WM / RPI; ++i) {
@@ -580,7 +685,9 @@ __global__ __launch_bounds__(kGemmThreads, Cfg::MINB) void gemm_nt_kernel(const 
       const int head = kind == 0 ? c0 / HD : (kind == 1 ? (c0 - qd) / HD : (c0 - qd - kvd) / HD);
       const int nheads = kind == 0 ? q.nq : q.nkv;
       uint16_t* obase = kind == 0 ? q.q_out : (kind == 1 ? q.k_out : q.v_out);
-      const int64_t b = gm / q.S, s = gm - b * q.S;
+      int64_t b;
+      uint32_t s;
+      tok(r, b, s);
       dst = obase + ((b * nheads + head) * q.S + s) * HD + (col % HD);
     } else if constexpr (EP == Epi::kSwiGLU) {
       const int n = (n0 + wn * WN) / 2 + col;

@@ -193,6 +193,7 @@ extern "C" int cdx_mu_qkv_rope_fwd(const uint16_t* x, int64_t ldx, const uint16_
   const int64_t N = (int64_t)(nq + 2 * nkv) * hd;
   const int64_t K = mu ? 2 * (int64_t)H : (int64_t)H;
   if (N > INT32_MAX) return fail(CDX_EUNSUPPORTED, "%s: too many heads", name);
+  if (S > INT32_MAX - 256) return fail(CDX_EUNSUPPORTED, "%s: S=%lld too long", name, (long long)S);
   if (ldx < H || ldw < K || (mu && ldmu != 0 && ldmu < H))
     return fail(CDX_EINVAL, "%s: leading dimension too small", name);
   if (ldx % 8 || ldw % 8 || (mu && ldmu % 8))
