@@ -133,9 +133,14 @@ struct GemmCfg {
 #endif
 using DefaultCfg = GemmCfg<CDX_GEMM_CFG>;
 
-__device__ __forceinline__ int xcd_remap(int b, int nb) {
-  const int q = nb / kNumXcd, r = nb % kNumXcd;
+// Logical tile of block b when `tiles` real tiles run on a grid of at least that many
+// blocks: the hardware deals blocks to the XCDs round robin (XCD b % 8), so XCD x
+// gets an equal share of the real tiles as one contiguous logical range (its L2 then
+// serves neighbouring tiles).  Blocks beyond their XCD's share get -1.
+__device__ __forceinline__ int xcd_remap(int b, int tiles) {
+  const int q = tiles / kNumXcd, r = tiles % kNumXcd;
   const int xcd = b % kNumXcd, k = b / kNumXcd;
+  if (k >= q + (xcd < r ? 1 : 0)) return -1;
   return (xcd < r ? xcd * (q + 1) : r * (q + 1) + (xcd - r) * q) + k;
 }
 
@@ -199,11 +204,21 @@ __global__ __launch_bounds__(kGemmThreads, Cfg::MINB) void gemm_nt_kernel(const 
   const int wm = wave >> 1, wn = wave & 1;
 
   // ---- tile decode -------------------------------------------------------
-  const int L = xcd_remap(blockIdx.x, gridDim.x);
+  // Grouped GEMMs launch an upper bound of M tiles; the real count follows from the
+  // segment offsets, so that the surplus blocks neither take an XCD's share nor sit
+  // in the middle of the logical order.
+  int mt_real = p.mt_count;
+  if (p.offsets != nullptr) {
+    mt_real = 0;
+    for (int x = 0; x < p.E; ++x) mt_real += (p.offsets[x + 1] - p.offsets[x] + kBM - 1) / kBM;
+    mt_real = min(mt_real, p.mt_count);
+  }
+  const int L = xcd_remap(blockIdx.x, mt_real * p.nt_count);
+  if (L < 0) return;
   const int per_group = kGroupM * p.nt_count;
   const int group = L / per_group;
   const int first_m = group * kGroupM;
-  const int gsz = min(p.mt_count - first_m, kGroupM);
+  const int gsz = min(mt_real - first_m, kGroupM);
   const int in_group = L - group * per_group;
   const int mt = first_m + in_group % gsz;
   const int nt = in_group / gsz;
