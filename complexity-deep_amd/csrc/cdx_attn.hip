@@ -22,9 +22,10 @@
 //   * Causal work: the block visits key tiles up to its last query; a wave skips the
 //     MFMAs of tiles entirely above its rows; the last query tiles, which do the most
 //     work, are launched first.
-//   * Softmax in the log2 domain: t = s * log2(e) / sqrt(D), running max m and sum l,
-//     O rescaled by exp2(m_old - m_new); one division by l at the end; one bf16
-//     rounding of O.
+//   * Softmax in the log2 domain: t = s * log2(e) / sqrt(D) folded into one FMA
+//     before exp2; running max m and sum l, with the rescale of O and l by
+//     exp2(m_old - m_new) done only when a row's max passes m by more than kLazy;
+//     one division by l at the end; one bf16 rounding of O.
 #include "cdx_gemm.h"
 
 namespace cdx {
@@ -44,6 +45,7 @@ struct AttnParams {
 
 constexpr int kAttnBM = 128;  // queries per block, 32 per wave
 constexpr int kAttnBN = 64;   // keys per tile
+constexpr float kLazy = 8.f;  // log2-domain headroom before the running max is moved
 
 template <int HD>
 __global__ __launch_bounds__(256, 2) void attn_fwd_kernel(const AttnParams p) {
@@ -159,7 +161,14 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_kernel(const AttnParams p) {
     if (t + 1 < nt) issue(t + 1, stage ^ 1);
     if (t < nt_wave) {
       const uint8_t* st = lds + stage * STAGE;
-      // S^T = K Q^T for the tile's two 32-key blocks
+      // S^T = K Q^T for the tile's two 32-key blocks; all K fragments are read first
+      // so that their LDS latency overlaps instead of stalling every MFMA pair.
+      bf16x8 kfr[2 * NKD];
+#pragma unroll
+      for (int k = 0; k < NKD; ++k) {
+        kfr[2 * k] = *reinterpret_cast<const bf16x8*>(st + kf_off[0][k]);
+        kfr[2 * k + 1] = *reinterpret_cast<const bf16x8*>(st + kf_off[1][k]);
+      }
       f32x16 sacc[2];
 #pragma unroll
       for (int nb = 0; nb < 2; ++nb)
@@ -167,55 +176,75 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_kernel(const AttnParams p) {
         for (int v = 0; v < 16; ++v) sacc[nb][v] = 0.f;
 #pragma unroll
       for (int k = 0; k < NKD; ++k) {
-        const bf16x8 k0 = *reinterpret_cast<const bf16x8*>(st + kf_off[0][k]);
-        const bf16x8 k1 = *reinterpret_cast<const bf16x8*>(st + kf_off[1][k]);
-        sacc[0] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(k0, qf[k], sacc[0], 0, 0, 0);
-        sacc[1] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(k1, qf[k], sacc[1], 0, 0, 0);
+        sacc[0] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kfr[2 * k], qf[k], sacc[0], 0, 0, 0);
+        sacc[1] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kfr[2 * k + 1], qf[k], sacc[1], 0, 0, 0);
       }
-      // scale to the log2 domain, mask, tile row max
+      // V^T fragments of the tile, in flight during the softmax.
+      bf16x8 vfr[4 * NDB];
+#pragma unroll
+      for (int sl = 0; sl < 4; ++sl)
+#pragma unroll
+        for (int db = 0; db < NDB; ++db)
+          vfr[sl * NDB + db] = *reinterpret_cast<const bf16x8*>(st + vf_off[db][sl]);
+      // Causal / length mask on the tiles that reach this wave's rows: key
+      // n0 + idx is visible iff idx <= lim (one compare per score, no branches).
       const int64_t n0 = (int64_t)t * kAttnBN;
-      const bool masked_tile = n0 + kAttnBN - 1 > mw;  // some key above some row of this wave
+      if (n0 + kAttnBN - 1 > mw) {
+        const int64_t last = (m < S ? m : S - 1) - n0;
+        const int lim = (int)(last < kAttnBN ? last : kAttnBN);
+#pragma unroll
+        for (int nb = 0; nb < 2; ++nb)
+#pragma unroll
+          for (int v = 0; v < 16; ++v) {
+            const int idx = nb * 32 + 8 * (v >> 2) + 4 * hi + (v & 3);
+            sacc[nb][v] = idx > lim ? -INFINITY : sacc[nb][v];
+          }
+      }
+      // Row max of the tile's raw scores.
       float mx = -INFINITY;
 #pragma unroll
       for (int nb = 0; nb < 2; ++nb)
 #pragma unroll
-        for (int v = 0; v < 16; ++v) {
-          float tv = sacc[nb][v] * p.scale_log2;
-          if (masked_tile) {
-            const int64_t n = n0 + nb * 32 + 8 * (v >> 2) + 4 * hi + (v & 3);
-            if (n > m || n >= S) tv = -INFINITY;
-          }
-          sacc[nb][v] = tv;
-          mx = fmaxf(mx, tv);
-        }
-      mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
-      const float m_new = fmaxf(m_run, mx);
-      const float alpha = __builtin_amdgcn_exp2f(m_run - m_new);
+        for (int v = 0; v < 16; ++v) mx = fmaxf(mx, sacc[nb][v]);
+      mx = fmaxf(mx, __shfl_xor(mx, 32, 64)) * p.scale_log2;
+      // Lazy rescale: the reference max m_run (log2 units) moves only when a row's max
+      // passes it by more than kLazy; until then P = 2^(t - m_run) <= 2^kLazy, which
+      // bf16 and fp32 hold, and the final division by l cancels the reference.  Tile 0
+      // holds key 0, visible to every row, so m_run is finite from then on.
+      if (__builtin_amdgcn_ballot_w64(mx > m_run + kLazy) != 0) {
+        const float m_new = fmaxf(m_run, mx);
+        const float alpha = __builtin_amdgcn_exp2f(m_run - m_new);
+        l_run *= alpha;
+        m_run = m_new;
+#pragma unroll
+        for (int db = 0; db < NDB; ++db)
+#pragma unroll
+          for (int v = 0; v < 16; ++v) o[db][v] *= alpha;
+      }
       float rs = 0.f;
       bf16x8 pf[4];
 #pragma unroll
       for (int nb = 0; nb < 2; ++nb)
 #pragma unroll
-        for (int v = 0; v < 16; ++v) {
-          const float pv = __builtin_amdgcn_exp2f(sacc[nb][v] - m_new);
-          rs += pv;
-          pf[nb * 2 + (v >> 3)][v & 7] = static_cast<bf16_t>(pv);
+        for (int g = 0; g < 2; ++g) {
+          uint32_t w[4];
+#pragma unroll
+          for (int j = 0; j < 4; ++j) {
+            const float p0 = __builtin_amdgcn_exp2f(__builtin_fmaf(sacc[nb][8 * g + 2 * j], p.scale_log2, -m_run));
+            const float p1 = __builtin_amdgcn_exp2f(__builtin_fmaf(sacc[nb][8 * g + 2 * j + 1], p.scale_log2, -m_run));
+            rs += p0 + p1;
+            w[j] = pack_bf16x2(p0, p1);
+          }
+          pf[nb * 2 + g] = __builtin_bit_cast(bf16x8, make_uint4(w[0], w[1], w[2], w[3]));
         }
       rs += __shfl_xor(rs, 32, 64);
-      l_run = l_run * alpha + rs;
-      m_run = m_new;
-#pragma unroll
-      for (int db = 0; db < NDB; ++db)
-#pragma unroll
-        for (int v = 0; v < 16; ++v) o[db][v] *= alpha;
+      l_run += rs;
       // O^T += V^T P over the tile's four 16-key slabs
 #pragma unroll
       for (int sl = 0; sl < 4; ++sl)
 #pragma unroll
-        for (int db = 0; db < NDB; ++db) {
-          const bf16x8 vf = *reinterpret_cast<const bf16x8*>(st + vf_off[db][sl]);
-          o[db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vf, pf[sl], o[db], 0, 0, 0);
-        }
+        for (int db = 0; db < NDB; ++db)
+          o[db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vfr[sl * NDB + db], pf[sl], o[db], 0, 0, 0);
     }
     // next tile landed (own DMA) and this wave is done with `stage`
     __builtin_amdgcn_s_waitcnt(waitcnt_imm(0, 0));
