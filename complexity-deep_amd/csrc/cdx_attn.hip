@@ -16,9 +16,12 @@
 //     layout is exactly the B-operand layout once the key order inside each 16-key
 //     group matches.  V therefore arrives transposed, [B, nkv, D, vt_ld], with that key
 //     order (vt_col in cdx_gemm.h), written so by the projection's epilogue.
-//   * K and V^T tiles are DMA'd (global_load_lds_dwordx4) into two LDS stages with
-//     the same 256-byte-line chunk swizzle as the GEMM engine; the next tile's DMA is
-//     in flight while the current one is consumed; one barrier per tile.
+//   * K and V^T tiles are DMA'd (buffer_load_dwordx4 ... lds, one buffer descriptor
+//     per (batch, kv head) slice) into two LDS stages with the same 256-byte-line
+//     chunk swizzle as the GEMM engine; the next tile's DMA is in flight while the
+//     current one is consumed; one barrier per tile.  The tile loop is unrolled by
+//     the two stages so that stage offsets are instruction immediates, and K
+//     fragments are read through a rolling window ahead of their MFMAs.
 //   * Causal work: the block visits key tiles up to its last query; a wave skips the
 //     MFMAs of tiles entirely above its rows; the last query tiles, which do the most
 //     work, are launched first.
@@ -26,6 +29,8 @@
 //     before exp2; running max m and sum l, with the rescale of O and l by
 //     exp2(m_old - m_new) done only when a row's max passes m by more than kLazy;
 //     one division by l at the end; one bf16 rounding of O.
+#include <type_traits>
+
 #include "cdx_gemm.h"
 
 namespace cdx {
@@ -98,33 +103,32 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_kernel(const AttnParams p) {
   // ---- DMA sources ---------------------------------------------------------------
   // K tile row r (key n0 + r): chunk c at position c ^ ((r / K_RPL) % K_CPR).
   // V^T tile row d (keys n0 .. n0 + 63, 128 bytes): chunk c at position c ^ ((d / 2) % 8).
-  const uint16_t* kbase = p.k + ((int64_t)b * p.nkv + kvh) * S * HD;
-  const uint16_t* vbase = p.vt + ((int64_t)b * p.nkv + kvh) * HD * p.vt_ld;
-  int k_row[KPW], k_off[KPW];
+  // Buffer loads straight to LDS: each lane's byte offset inside the (batch, kv head)
+  // slice is fixed and the tile's key position travels in the scalar offset.  The K
+  // descriptor covers exactly S rows, so rows past the end read as zeros (and are
+  // masked); V^T columns up to vt_ld are in range and finite by contract.
+  const __amdgpu_buffer_rsrc_t rs_k =
+      make_rsrc(p.k + ((int64_t)b * p.nkv + kvh) * S * HD, (uint32_t)(S * HD * 2));
+  const __amdgpu_buffer_rsrc_t rs_v = make_rsrc(p.vt + ((int64_t)b * p.nkv + kvh) * HD * p.vt_ld);
+  uint32_t k_off[KPW], v_off[VPW];
 #pragma unroll
   for (int j = 0; j < KPW; ++j) {
     const int r = (wave * KPW + j) * K_ROWS_DMA + lane / K_CPR;
-    k_row[j] = r;
-    k_off[j] = ((lane % K_CPR) ^ ((r / K_RPL) % K_CPR)) * 8;
+    k_off[j] = (uint32_t)(r * HD + ((lane % K_CPR) ^ ((r / K_RPL) % K_CPR)) * 8) * 2;
   }
-  int64_t v_off[VPW];
 #pragma unroll
   for (int j = 0; j < VPW; ++j) {
     const int d = (wave * VPW + j) * 8 + lane / 8;
-    v_off[j] = (int64_t)d * p.vt_ld + ((lane % 8) ^ ((d / 2) % 8)) * 8;
+    v_off[j] = (uint32_t)((int64_t)d * p.vt_ld + ((lane % 8) ^ ((d / 2) % 8)) * 8) * 2;
   }
   auto issue = [&](int t, int stage) __attribute__((always_inline)) {
-    const int64_t n0 = (int64_t)t * kAttnBN;
+    const uint32_t n0 = (uint32_t)t * kAttnBN;
     uint8_t* ks = lds + stage * STAGE;
     uint8_t* vs = ks + K_BYTES;
 #pragma unroll
-    for (int j = 0; j < KPW; ++j) {
-      int64_t n = n0 + k_row[j];
-      n = n < S ? n : S - 1;  // keys past S are loaded but masked
-      dma16(kbase + n * HD + k_off[j], ks + (wave * KPW + j) * 1024);
-    }
+    for (int j = 0; j < KPW; ++j) buf_dma16(rs_k, k_off[j], n0 * HD * 2, ks + (wave * KPW + j) * 1024);
 #pragma unroll
-    for (int j = 0; j < VPW; ++j) dma16(vbase + v_off[j] + n0, vs + (wave * VPW + j) * 1024);
+    for (int j = 0; j < VPW; ++j) buf_dma16(rs_v, v_off[j], n0 * 2, vs + (wave * VPW + j) * 1024);
   };
 
   // ---- fragment offsets in a stage -------------------------------------------------
@@ -156,28 +160,34 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_kernel(const AttnParams p) {
   __builtin_amdgcn_s_waitcnt(waitcnt_imm(0, 15));
   __syncthreads();
 
-  for (int t = 0; t < nt; ++t) {
-    const int stage = t & 1;
+  // One key tile; STG is the tile's LDS stage as a compile-time constant, so the
+  // stage offset folds into the LDS instructions' immediate offsets.
+  auto tile = [&](int t, auto stg) __attribute__((always_inline)) {
+    constexpr int stage = decltype(stg)::value;
     if (t + 1 < nt) issue(t + 1, stage ^ 1);
     if (t < nt_wave) {
       const uint8_t* st = lds + stage * STAGE;
-      // S^T = K Q^T for the tile's two 32-key blocks; all K fragments are read first
-      // so that their LDS latency overlaps instead of stalling every MFMA pair.
-      bf16x8 kfr[2 * NKD];
+      // S^T = K Q^T for the tile's two 32-key blocks.  The 2 NKD K fragments are read
+      // through a rolling window: fragment i + KWIN is read behind the MFMA of
+      // fragment i, so KWIN reads are in flight while the MFMAs run (the full set
+      // does not fit next to O, the Q fragments and the V^T fragments).
+      constexpr int NKF = 2 * NKD, KWIN = NKF < 6 ? NKF : 6;
+      auto kfrag = [&](int i) __attribute__((always_inline)) {
+        return *reinterpret_cast<const bf16x8*>(st + kf_off[i & 1][i >> 1]);
+      };
+      bf16x8 kfr[NKF];
 #pragma unroll
-      for (int k = 0; k < NKD; ++k) {
-        kfr[2 * k] = *reinterpret_cast<const bf16x8*>(st + kf_off[0][k]);
-        kfr[2 * k + 1] = *reinterpret_cast<const bf16x8*>(st + kf_off[1][k]);
-      }
+      for (int i = 0; i < KWIN; ++i) kfr[i] = kfrag(i);
       f32x16 sacc[2];
 #pragma unroll
       for (int nb = 0; nb < 2; ++nb)
 #pragma unroll
         for (int v = 0; v < 16; ++v) sacc[nb][v] = 0.f;
 #pragma unroll
-      for (int k = 0; k < NKD; ++k) {
-        sacc[0] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kfr[2 * k], qf[k], sacc[0], 0, 0, 0);
-        sacc[1] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kfr[2 * k + 1], qf[k], sacc[1], 0, 0, 0);
+      for (int i = 0; i < NKF; ++i) {
+        sacc[i & 1] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kfr[i], qf[i >> 1], sacc[i & 1], 0, 0, 0);
+        if (i + KWIN < NKF) kfr[i + KWIN] = kfrag(i + KWIN);
+        __builtin_amdgcn_sched_barrier(0);
       }
       // V^T fragments of the tile, in flight during the softmax.
       bf16x8 vfr[4 * NDB];
@@ -249,6 +259,10 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_kernel(const AttnParams p) {
     // next tile landed (own DMA) and this wave is done with `stage`
     __builtin_amdgcn_s_waitcnt(waitcnt_imm(0, 0));
     __syncthreads();
+  };
+  for (int t = 0; t < nt; t += 2) {
+    tile(t, std::integral_constant<int, 0>{});
+    if (t + 1 < nt) tile(t + 1, std::integral_constant<int, 1>{});
   }
 
   // ---- O = O^T / l -> out[b, m, h * HD + d] ----------------------------------------
@@ -293,6 +307,9 @@ extern "C" int cdx_attention_fwd(const uint16_t* q, const uint16_t* k, const uin
   if (B == 0 || S == 0) return CDX_OK;
   if ((S + kAttnBM - 1) / kAttnBM > INT32_MAX || B * nq > INT32_MAX)
     return fail(CDX_EUNSUPPORTED, "%s: problem too large", name);
+  // The kernel addresses one (batch, kv head) slice of K and of V^T with 32-bit offsets.
+  if (S * hd * 2 > (int64_t)UINT32_MAX || vt_ld * hd * 2 > (int64_t)UINT32_MAX)
+    return fail(CDX_EUNSUPPORTED, "%s: a K or V^T head slice must fit 4 GB (S=%lld)", name, (long long)S);
   if (!q || !k || !vt || !out) return fail(CDX_EINVAL, "%s: null pointer", name);
   if (!aligned16(q) || !aligned16(k) || !aligned16(vt) || !aligned16(out))
     return fail(CDX_EUNSUPPORTED, "%s: pointers must be 16-byte aligned", name);
