@@ -108,7 +108,10 @@ struct GemmParams {
 
 constexpr int kBM = 256;
 constexpr int kGemmThreads = 256;
-constexpr int kGroupM = 4;
+#ifndef CDX_GROUP_M
+#define CDX_GROUP_M 4
+#endif
+constexpr int kGroupM = CDX_GROUP_M;  // M tiles per group in the tile order
 constexpr int kNumXcd = 8;
 
 // Tile configuration: BN output columns per block, BK-deep LDS stages, STAGES of
@@ -638,6 +641,15 @@ __global__ __launch_bounds__(kGemmThreads, Cfg::MINB) void gemm_nt_kernel(const 
         }
     }
   } else {
+    // kBiasClamp: the lane's NI groups of 4 bias values, loaded once for every row.
+    float4 bias4[EP == Epi::kBiasClamp ? NI : 1];
+    if constexpr (EP == Epi::kBiasClamp) {
+#pragma unroll
+      for (int ni = 0; ni < NI; ++ni) {
+        const int n = n0 + wn * WN + ni * 16 + 4 * q4;
+        bias4[ni] = n < p.N ? *reinterpret_cast<const float4*>(p.bias + n) : make_float4(0.f, 0.f, 0.f, 0.f);
+      }
+    }
 #pragma unroll
     for (int mi = 0; mi < MI; ++mi) {
       const int r = mi * 16 + rl;
@@ -646,13 +658,9 @@ __global__ __launch_bounds__(kGemmThreads, Cfg::MINB) void gemm_nt_kernel(const 
         const int col = ni * 16 + 4 * q4;
         float y[4] = {acc[mi][ni][0], acc[mi][ni][1], acc[mi][ni][2], acc[mi][ni][3]};
         if constexpr (EP == Epi::kBiasClamp) {
-          const int n = n0 + wn * WN + col;
-          if (n < p.N) {
-            const float4 bv = *reinterpret_cast<const float4*>(p.bias + n);
-            const float bb[4] = {bv.x, bv.y, bv.z, bv.w};
+          const float bb[4] = {bias4[ni].x, bias4[ni].y, bias4[ni].z, bias4[ni].w};
 #pragma unroll
-            for (int j = 0; j < 4; ++j) y[j] = fminf(fmaxf(y[j] + bb[j], p.lo), p.hi);
-          }
+          for (int j = 0; j < 4; ++j) y[j] = fminf(fmaxf(y[j] + bb[j], p.lo), p.hi);
         }
         stage4(r, col, y[0], y[1], y[2], y[3]);
       }
