@@ -40,6 +40,14 @@ __device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
   return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, bf16x2_t));
 }
 
+// 16-byte store with the non-temporal hint (streamed output that the kernel does
+// not read back).
+__device__ __forceinline__ void store_nt16(void* p, const uint4& v) {
+  typedef __attribute__((ext_vector_type(4))) unsigned int u32x4_t;
+  const u32x4_t w = {v.x, v.y, v.z, v.w};
+  __builtin_nontemporal_store(w, reinterpret_cast<u32x4_t*>(p));
+}
+
 // Unpack the 8 bf16 values held in a 16-byte vector into floats.
 __device__ __forceinline__ void unpack8(const uint4& v, float* f) {
   const uint32_t w[4] = {v.x, v.y, v.z, v.w};

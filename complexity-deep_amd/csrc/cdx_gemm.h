@@ -668,7 +668,8 @@ __global__ __launch_bounds__(kGemmThreads, Cfg::MINB) void gemm_nt_kernel(const 
   }
 
   // Own LDS writes are complete before the reads (LDS operations of a wave execute
-  // in order; the wait also keeps the compiler from reordering them).
+  // in order; the wait also keeps the compiler from reordering them).  The outputs
+  // are streamed (non-temporal stores), which keeps the operands' panels in L2.
   __builtin_amdgcn_s_waitcnt(waitcnt_imm(63, 0));
   if constexpr (EP == Epi::kQKRope) {
     if (vt_fast) {
@@ -684,7 +685,7 @@ __global__ __launch_bounds__(kGemmThreads, Cfg::MINB) void gemm_nt_kernel(const 
         const int head = (c0 - (q.nq + q.nkv) * HD) / HD, d = row % HD;
         const uint4 v = *reinterpret_cast<const uint4*>(ep + row * 256 + ((k ^ (row & 15)) << 4));
         uint16_t* dst = q.v_out + ((tok_b0 * q.nkv + head) * HD + d) * q.vt_ld + tok_s0 + k * 8;
-        *reinterpret_cast<uint4*>(dst) = v;
+        store_nt16(dst, v);
       }
       return;
     }
@@ -722,7 +723,7 @@ __global__ __launch_bounds__(kGemmThreads, Cfg::MINB) void gemm_nt_kernel(const 
       const int64_t orow = EP == Epi::kScatter ? (int64_t)p.perm[gm] : gm;
       dst = p.c + orow * p.ldc + n;
     }
-    *reinterpret_cast<uint4*>(dst) = v;
+    store_nt16(dst, v);
   }
 }
 
