@@ -88,6 +88,11 @@ def work_of(name: str, s: dict):
         # causal: query s sees s + 1 keys; QK^T and PV are 2 * D FLOP per (query, key) each
         S = s["S"]
         return 4.0 * s["B"] * s["nq"] * s["D"] * S * (S + 1) / 2, "flop"
+    if name == "lm_head":
+        return 2.0 * s["M"] * s["K"] * s["N"], "flop"
+    if name == "embedding":
+        # ids in; one table row read and one output row written per token
+        return float(s["T"] * (8 + 2 * 2 * s["H"])), "byte"
     if name == "route_plan":
         # ids in; expert_id, perm, inv_perm out; the map is read once per token at most
         return float(s["T"] * (8 + 4 + 4 + 4) + 2 * 4 * (s["E"] + 1)), "byte"

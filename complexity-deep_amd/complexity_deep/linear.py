@@ -1,0 +1,53 @@
+"""The model's two ends on the gfx950 kernels: the token-embedding gather and the
+tied LM head (models/modeling.py:74,101-103,177,206).
+
+``embedding(ids, table)`` is nn.Embedding's lookup through cdx_embedding_fwd (an
+exact row copy; ids outside [0, vocab) give zero rows where nn.Embedding raises).
+``linear(x, w)`` is a bias-free nn.Linear (x @ w^T, w stored [out, in]) through the
+MFMA tile engine (cdx_linear_fwd; fp32 accumulation, one bf16 rounding).
+"""
+
+from __future__ import annotations
+
+import torch
+
+from . import _native as nat
+
+
+def embedding(ids: torch.Tensor, table: torch.Tensor) -> torch.Tensor:
+    """table[ids] for int64 ids of any shape; returns [*ids.shape, H]."""
+    nat.require_device(table, what="embedding")
+    nat.require_device(ids, table, dtype=None, what="embedding")
+    if table.dim() != 2:
+        raise ValueError("embedding: table must be [vocab, hidden]")
+    V, H = table.shape
+    flat = ids.reshape(-1)
+    flat = flat if flat.dtype == torch.int64 else flat.to(torch.int64)
+    flat = flat if flat.is_contiguous() else flat.contiguous()
+    table = table if table.is_contiguous() else table.contiguous()
+    out = torch.empty(flat.shape[0], H, dtype=table.dtype, device=table.device)
+    with nat.launch_region("embedding", table.device, T=flat.shape[0], H=H):
+        nat.check(nat.lib().cdx_embedding_fwd(flat.data_ptr(), flat.shape[0], table.data_ptr(), V, H,
+                                              out.data_ptr(), nat.stream_of(table)), "cdx_embedding_fwd")
+    return out.view(*ids.shape, H)
+
+
+def linear_supported(in_features: int, out_features: int) -> bool:
+    """Shapes cdx_linear_fwd takes: K a multiple of 64, N a multiple of 8."""
+    return in_features % 64 == 0 and out_features % 8 == 0
+
+
+def linear(x: torch.Tensor, w: torch.Tensor) -> torch.Tensor:
+    """x @ w^T for x [..., K], w [N, K] (nn.Linear weight layout), bf16."""
+    nat.require_device(x, w, what="linear")
+    N, K = w.shape
+    if x.shape[-1] != K:
+        raise ValueError(f"linear: x has {x.shape[-1]} features, weight expects {K}")
+    x2 = x.reshape(-1, K)
+    x2 = x2 if x2.is_contiguous() else x2.contiguous()
+    w = w if w.is_contiguous() else w.contiguous()
+    out = torch.empty(x2.shape[0], N, dtype=x.dtype, device=x.device)
+    with nat.launch_region("lm_head", x.device, M=x2.shape[0], K=K, N=N):
+        nat.check(nat.lib().cdx_linear_fwd(x2.data_ptr(), K, w.data_ptr(), K, x2.shape[0], K, N, out.data_ptr(), N,
+                                           nat.stream_of(x)), "cdx_linear_fwd")
+    return out.view(*x.shape[:-1], N)

@@ -15,9 +15,12 @@ The forward (modeling.py:155-219) runs the hot path on the gfx950 kernels:
   * the mu-QKV projection carries QK-norm and RoPE in its epilogue and feeds the
     causal GQA attention kernel (no mask, no KV cache);
   * mu guidance is one kernel that also applies the [-2, 2] clamp between layers;
-  * the last layer's mu, which the reference computes and discards, is skipped.
-Embedding, o_proj and lm_head run as PyTorch-ROCm ops, as does attention with a
-mask or a KV cache (generation).
+  * the last layer's mu, which the reference computes and discards, is skipped;
+  * the embedding gather and the tied LM head run on their own kernels
+    (cdx_embedding_fwd, cdx_linear_fwd; vocabularies not a multiple of 8 keep
+    nn.Linear for the head).
+o_proj runs as a PyTorch-ROCm op, as does attention with a mask or a KV cache
+(generation).
 """
 
 from __future__ import annotations
@@ -34,6 +37,7 @@ import torch.nn.functional as F
 
 from ._grad import forward_only
 from .layer import TransformerBlock
+from .linear import embedding, linear, linear_supported
 from .normalization import RMSNorm, rms_norm
 from .token_routed_mlp import RoutePlan, route_plan
 
@@ -212,7 +216,7 @@ class ComplexityModel(nn.Module):
                 use_cache: bool = False) -> CausalLMOutput:
         forward_only("ComplexityModel", *self.parameters())
         B, S = input_ids.shape
-        h = self.embed_tokens(input_ids)
+        h = embedding(input_ids, self.embed_tokens.weight)
         mu_prev = self.mu_init.expand(B, S, -1) if self.config.use_mu_guidance else None
         plans = self.route_plans(input_ids)
         new_kvs = [] if use_cache else None
@@ -231,7 +235,9 @@ class ComplexityModel(nn.Module):
                 mu_prev = mu  # clamped to [-2, 2] inside the mu-guidance kernel
             if use_cache:
                 new_kvs.append(new_kv)
-        logits = self.lm_head(normed)
+        w_head = self.lm_head.weight
+        logits = linear(normed, w_head) if linear_supported(w_head.shape[1], w_head.shape[0]) \
+            else self.lm_head(normed)
         loss = None
         if labels is not None:
             loss = F.cross_entropy(logits[..., :-1, :].contiguous().view(-1, self.config.vocab_size),

@@ -7,6 +7,7 @@
 //   cdx_grouped_gemm_fwd plain grouped GEMM over expert segments
 //   cdx_mu_guidance_fwd  mu = clamp(h @ W_mu^T + clamp(mu_param), lo, hi), the
 //                        producer of the next layer's mu operand
+//   cdx_linear_fwd       y = x @ W^T (the tied LM head)
 #include "cdx_gemm.h"
 
 namespace cdx {
@@ -278,4 +279,36 @@ extern "C" int cdx_mu_guidance_fwd(const uint16_t* h, int64_t T, int32_t H, cons
   if (cdiv(T, kBM) > INT32_MAX) return fail(CDX_EUNSUPPORTED, "%s: T too large", name);
   p.mt_count = (int32_t)cdiv(T, kBM);
   return launch<ALoad::kDense, Epi::kBiasClamp>(p, reinterpret_cast<hipStream_t>(stream), name);
+}
+
+extern "C" int cdx_linear_fwd(const uint16_t* x, int64_t ldx, const uint16_t* w, int64_t ldw, int64_t M, int32_t K,
+                              int32_t N, uint16_t* out, int64_t ldo, void* stream) {
+  using namespace cdx;
+  clear_error();
+  const char* name = "cdx_linear_fwd";
+  if (M < 0 || K <= 0 || N <= 0) return fail(CDX_EINVAL, "%s: bad shape M=%lld K=%d N=%d", name, (long long)M, K, N);
+  if (K % 64 != 0) return fail(CDX_EUNSUPPORTED, "%s: K=%d must be a multiple of 64", name, K);
+  if (N % 8 != 0) return fail(CDX_EUNSUPPORTED, "%s: N=%d must be a multiple of 8", name, N);
+  if (ldx < K || ldw < K || ldo < N) return fail(CDX_EINVAL, "%s: leading dimension too small", name);
+  if (ldx % 8 || ldw % 8 || ldo % 8)
+    return fail(CDX_EUNSUPPORTED, "%s: leading dimensions must be multiples of 8", name);
+  if (M == 0) return CDX_OK;
+  if (!x || !w || !out) return fail(CDX_EINVAL, "%s: null pointer", name);
+  if (!aligned16(x) || !aligned16(w) || !aligned16(out))
+    return fail(CDX_EUNSUPPORTED, "%s: pointers must be 16-byte aligned", name);
+  GemmParams p{};
+  p.a = x;
+  p.lda = ldx;
+  p.k_split = K;
+  p.E = 1;
+  p.M = M;
+  p.b = w;
+  p.ldb = ldw;
+  p.N = N;
+  p.K = K;
+  p.c = out;
+  p.ldc = ldo;
+  if (cdiv(M, kBM) > INT32_MAX) return fail(CDX_EUNSUPPORTED, "%s: M too large", name);
+  p.mt_count = (int32_t)cdiv(M, kBM);
+  return launch<ALoad::kDense, Epi::kStore>(p, reinterpret_cast<hipStream_t>(stream), name);
 }

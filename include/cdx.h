@@ -235,6 +235,29 @@ int cdx_attention_fwd(const uint16_t* q_dev, const uint16_t* k_dev, const uint16
                       int64_t S, int32_t nq, int32_t nkv, int32_t hd, int64_t vt_ld, float scale,
                       uint16_t* out_dev, void* stream);
 
+/* ---- the model's ends: embedding gather and the tied LM head --------------- */
+
+/*
+ * out[t, :] = table[ids[t], :] for t < T; table [V, H] bf16 (the embedding weight),
+ * ids int64 on the device, out [T, H] bf16.  An id outside [0, V) yields a row of
+ * zeros (nn.Embedding raises there).  H must be a multiple of 8 and <= 16384.
+ *
+ * Replaces: models/modeling.py:74,177 (nn.Embedding and its lookup).
+ */
+int cdx_embedding_fwd(const int64_t* ids_dev, int64_t T, const uint16_t* table_dev, int64_t V, int32_t H,
+                      uint16_t* out_dev, void* stream);
+
+/*
+ * out[M, N] = x[M, K] @ w[N, K]^T, bf16 in and out, fp32 accumulation, one rounding:
+ * nn.Linear without bias with its weight as stored ([out, in]).  The model calls it
+ * for the tied LM head, w = the embedding table.  K % 64 == 0, N % 8 == 0, leading
+ * dimensions multiples of 8, pointers 16-byte aligned.
+ *
+ * Replaces: models/modeling.py:101-103,206 (lm_head, weight tied to embed_tokens).
+ */
+int cdx_linear_fwd(const uint16_t* x_dev, int64_t ldx, const uint16_t* w_dev, int64_t ldw, int64_t M, int32_t K,
+                   int32_t N, uint16_t* out_dev, int64_t ldo, void* stream);
+
 #ifdef __cplusplus
 }
 #endif
