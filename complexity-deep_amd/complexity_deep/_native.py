@@ -45,6 +45,7 @@ _SIGNATURES = {
                                          _vp, _vp]),
     "cdx_mu_guidance_fwd": (ctypes.c_int, [_vp, _i64, _i32, _vp, _vp, ctypes.c_float, ctypes.c_float, _vp,
                                            _vp]),
+    "cdx_binpack_map": (ctypes.c_int, [_vp, _i64, _i32, _vp]),
     "cdx_embedding_fwd": (ctypes.c_int, [_vp, _i64, _vp, _i64, _i32, _vp, _vp]),
     "cdx_linear_fwd": (ctypes.c_int, [_vp, _i64, _vp, _i64, _i64, _i32, _i32, _vp, _i64, _vp]),
 }

@@ -39,7 +39,7 @@ from ._grad import forward_only
 from .layer import TransformerBlock
 from .linear import embedding, linear, linear_supported
 from .normalization import RMSNorm, rms_norm
-from .token_routed_mlp import RoutePlan, route_plan
+from .token_routed_mlp import RoutePlan, TokenRoutedMLP, route_plan
 
 
 @dataclass
@@ -194,6 +194,23 @@ class ComplexityModel(nn.Module):
             self._map_groups = canon
             self._map_key = key
         return self._map_groups
+
+    def set_token_frequencies(self, token_frequencies: torch.Tensor) -> torch.Tensor:
+        """Build the greedy bin-packing map of ``token_frequencies`` ([vocab] corpus
+        frequencies) once, with the native builder, and install it in every routed
+        layer's ``token_to_expert`` buffer (saved in the state_dict as before).  The
+        reference builds it per layer when TokenRoutedMLP is given frequencies
+        (core/token_routed_mlp.py:80-116); ComplexityModel never passes any, so this
+        is how a model gets the bin-packed map.  Returns the map."""
+        mlps = [layer.mlp for layer in self.layers if getattr(layer, "use_token_routed_mlp", False)]
+        if not mlps:
+            raise ValueError("set_token_frequencies: the model has no token-routed MLP")
+        tmap = TokenRoutedMLP._build_token_mapping(self.config.vocab_size, self.config.num_experts,
+                                                   token_frequencies)
+        with torch.no_grad():
+            for mlp in mlps:
+                mlp.token_to_expert.copy_(tmap.to(mlp.token_to_expert.device))
+        return tmap
 
     def route_plans(self, input_ids: torch.Tensor) -> List[Optional[RoutePlan]]:
         groups = self._map_grouping()

@@ -17,7 +17,6 @@ happens anywhere in the forward.
 
 from __future__ import annotations
 
-import heapq
 from dataclasses import dataclass
 from typing import Optional, Tuple
 
@@ -240,26 +239,19 @@ class TokenRoutedMLP(nn.Module):
     @staticmethod
     def _build_token_mapping(vocab_size: int, num_experts: int,
                              token_frequencies: Optional[torch.Tensor]) -> torch.Tensor:
-        """Greedy Zipf bin-packing (token_routed_mlp.py:87-119).
-
-        Tokens are taken in descending frequency and each goes to the least-loaded
-        expert, the lowest index winning ties; loads accumulate in double precision.
-        Implemented with a min-heap keyed by (load, expert), which yields exactly the
-        first-minimum choice.  Without frequencies: token_id % num_experts."""
+        """Greedy Zipf bin-packing (token_routed_mlp.py:87-119) through the native
+        builder cdx_binpack_map: tokens in descending frequency (ties: lower id
+        first), each to the least-loaded expert (ties: lowest index), loads
+        accumulated in double.  Without frequencies: token_id % num_experts."""
         if token_frequencies is None:
             return torch.arange(vocab_size, dtype=torch.long) % num_experts
-        freq = torch.as_tensor(token_frequencies).detach().to("cpu", torch.float32)
-        if freq.shape[0] != vocab_size:
-            raise ValueError(f"token_frequencies has {freq.shape[0]} entries, vocab_size is {vocab_size}")
-        order = torch.sort(freq, descending=True, stable=True).indices.tolist()
-        values = freq.double().tolist()
-        heap = [(0.0, e) for e in range(num_experts)]
-        mapping = [0] * vocab_size
-        for tid in order:
-            load, e = heapq.heappop(heap)
-            mapping[tid] = e
-            heapq.heappush(heap, (load + values[tid], e))
-        return torch.tensor(mapping, dtype=torch.long)
+        freq = torch.as_tensor(token_frequencies).detach().to("cpu", torch.float32).contiguous()
+        if freq.shape != (vocab_size,):
+            raise ValueError(f"token_frequencies has shape {tuple(freq.shape)}, expected ({vocab_size},)")
+        mapping = torch.empty(vocab_size, dtype=torch.long)
+        nat.check(nat.lib().cdx_binpack_map(freq.data_ptr(), vocab_size, num_experts, mapping.data_ptr()),
+                  "cdx_binpack_map")
+        return mapping
 
     def packed_weights(self) -> Tuple[torch.Tensor, torch.Tensor]:
         """Kernel-layout weights, rebuilt only when a parameter changes (never saved)."""

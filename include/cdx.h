@@ -235,6 +235,20 @@ int cdx_attention_fwd(const uint16_t* q_dev, const uint16_t* k_dev, const uint16
                       int64_t S, int32_t nq, int32_t nkv, int32_t hd, int64_t vt_ld, float scale,
                       uint16_t* out_dev, void* stream);
 
+/* ---- expert map (host) ---------------------------------------------------- */
+
+/*
+ * Host function (no device work): the token -> expert map of greedy bin-packing.
+ * freq [V] float32 and map [V] int64 are host arrays.  Tokens are taken in
+ * descending frequency (ties: lower token id first) and each is assigned to the
+ * expert with the least accumulated load (ties: lowest expert index); loads are
+ * accumulated in double.  NaN frequencies are rejected.  1 <= E <= 65536.
+ *
+ * Replaces: core/token_routed_mlp.py:87-116 (_build_token_mapping with
+ * token_frequencies).
+ */
+int cdx_binpack_map(const float* freq, int64_t V, int32_t E, int64_t* map);
+
 /* ---- the model's ends: embedding gather and the tied LM head --------------- */
 
 /*

@@ -1,8 +1,9 @@
 """Pins the integer oracle (oracle/route_oracle.c) without retyping its formulas.
 
 * bin-packing (token_routed_mlp.py:105-116): the C argmin loop against a
-  pure-Python statement and against the product's heap-based builder (three
-  independent implementations of the same greedy rule), plus the load-balance
+  pure-Python statement and against the product's native builder (cdx_binpack_map,
+  a stable sort plus a (load, expert) min-heap: three independent implementations
+  of the same greedy rule), plus the load-balance
   facts the Zipf(1.1) pmf fixes at V=32000: E=4 splits the mass exactly in four;
   E=8 leaves token 0 (14.2% of the mass) alone in expert 0; map[0..9] values.
 * routing plan (token_routed_mlp.py:149-170, triton_token_routed.py:37-61): against
@@ -42,6 +43,25 @@ def test_binpack_with_ties_and_random_freqs(oracle):
         c = oracle.binpack_map(f, E)
         np.testing.assert_array_equal(c, oracle.binpack_map_py(f, E))
         np.testing.assert_array_equal(c, TokenRoutedMLP._build_token_mapping(500, E, torch.from_numpy(f)).numpy())
+
+
+@pytest.mark.parametrize("E", [8, 64])
+def test_binpack_native_zipf_32000(oracle, E):
+    """The 1B configuration's map (and a 64-expert one) from the native builder."""
+    from complexity_deep.token_routed_mlp import TokenRoutedMLP
+    f = zipf(32000)
+    np.testing.assert_array_equal(oracle.binpack_map(f, E),
+                                  TokenRoutedMLP._build_token_mapping(32000, E, torch.from_numpy(f)).numpy())
+
+
+def test_binpack_native_negative_and_nan(oracle):
+    from complexity_deep.token_routed_mlp import TokenRoutedMLP
+    rng = np.random.default_rng(5)
+    f = rng.normal(size=700).astype(np.float32)  # negative loads are legal arithmetic
+    np.testing.assert_array_equal(oracle.binpack_map(f, 6), TokenRoutedMLP._build_token_mapping(700, 6, torch.from_numpy(f)).numpy())
+    f[10] = np.nan
+    with pytest.raises(RuntimeError, match="NaN"):
+        TokenRoutedMLP._build_token_mapping(700, 6, torch.from_numpy(f))
 
 
 def _loads(f, m, E):
@@ -126,3 +146,20 @@ def test_route_plan_skewed_stress(oracle):
     assert c[1] == round(0.9 * 65536)
     assert all(c[e] == round(0.01 * 65536) for e in range(2, 8))
     assert c[0] == 65536 - c[1:].sum()  # expert 0 owns only the padding id 0
+
+
+def test_model_set_token_frequencies(oracle):
+    """ComplexityModel.set_token_frequencies installs the oracle's bin-packed map in
+    every routed layer (and the map is what the state_dict saves)."""
+    import complexity_deep as cd
+    cfg = cd.ComplexityConfig.complexity_tiny()
+    cfg.vocab_size = 1000
+    torch.manual_seed(0)
+    model = cd.ComplexityModel(cfg)
+    f = zipf(cfg.vocab_size)
+    tmap = model.set_token_frequencies(torch.from_numpy(f))
+    want = oracle.binpack_map(f, cfg.num_experts)
+    np.testing.assert_array_equal(tmap.numpy(), want)
+    sd = model.state_dict()
+    keys = [k for k in sd if k.endswith("mlp.token_to_expert")]
+    assert keys and all(np.array_equal(sd[k].numpy(), want) for k in keys)
