@@ -263,11 +263,15 @@ __global__ __launch_bounds__(kGemmThreads, Cfg::MINB) void gemm_nt_kernel(const 
   // instruction's scalar offset, so a DMA costs no vector instruction.  Dense and
   // concat A and B offsets are relative to the tile's first row (< 4 GB for any
   // practical leading dimension); gathered A offsets are relative to the matrix,
-  // which the host bounds to 4 GB.
+  // which the host bounds to 4 GB.  The concat descriptor's base sits k_split
+  // columns before mu's first column, so that both halves of K take the same scalar
+  // offset (2 k0) and the choice between them is a select, not a branch.
   const int dr = lane / CPR;
   const uint16_t* bexp = p.b + (int64_t)e * p.b_estride;
-  const __amdgpu_buffer_rsrc_t rs_a = make_rsrc(AL == ALoad::kGather ? p.a : p.a + m0 * p.lda);
-  const __amdgpu_buffer_rsrc_t rs_a2 = make_rsrc(AL == ALoad::kConcat ? p.a2 + m0 * p.lda2 : p.a);
+  const uintptr_t a_base = (uintptr_t)(AL == ALoad::kGather ? p.a : p.a + m0 * p.lda);
+  const uintptr_t a2_base =
+      AL == ALoad::kConcat ? (uintptr_t)(p.a2 + m0 * p.lda2) - (uintptr_t)p.k_split * 2 : a_base;
+  const __amdgpu_buffer_rsrc_t rs_a = make_rsrc((const void*)a_base);
   const __amdgpu_buffer_rsrc_t rs_b = make_rsrc(bexp + (int64_t)n0 * p.ldb);
   uint32_t a_off[LD_A], a2_off[LD_A], b_off[LD_B];
 #pragma unroll
@@ -304,8 +308,10 @@ __global__ __launch_bounds__(kGemmThreads, Cfg::MINB) void gemm_nt_kernel(const 
     const bool live = kt < KT;
     uint8_t* dst = lds + stage * STAGE_BYTES;
     if (d < LD_A) {
-      if (AL == ALoad::kConcat && k0 >= p.k_split) {
-        buf_dma16(live ? rs_a2 : rs_none, a2_off[d], (uint32_t)(k0 - p.k_split) * 2, dst + a_dma_off + d * 1024);
+      if constexpr (AL == ALoad::kConcat) {
+        const bool second = k0 >= p.k_split;
+        const __amdgpu_buffer_rsrc_t r = make_rsrc((const void*)(second ? a2_base : a_base));
+        buf_dma16(live ? r : rs_none, second ? a2_off[d] : a_off[d], (uint32_t)k0 * 2, dst + a_dma_off + d * 1024);
       } else {
         buf_dma16(live ? rs_a : rs_none, a_off[d], (uint32_t)k0 * 2, dst + a_dma_off + d * 1024);
       }
