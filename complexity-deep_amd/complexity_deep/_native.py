@@ -35,6 +35,8 @@ _SIGNATURES = {
     "cdx_unpermute_rows": (ctypes.c_int, [_vp, _vp, _i64, _i64, _vp, _vp]),
     "cdx_moe_swiglu_fwd": (ctypes.c_int, [_vp, _i64, _i32, _i32, _i32, _i32, _vp, _vp, _vp, _vp, _vp,
                                           _vp, _vp]),
+    "cdx_moe_swiglu_residual_fwd": (ctypes.c_int, [_vp, _i64, _i32, _i32, _i32, _i32, _vp, _vp, _vp, _vp,
+                                                   _vp, _vp, _vp]),
     "cdx_grouped_gemm_fwd": (ctypes.c_int, [_vp, _i64, _i32, _i32, _i32, _vp, _vp, _vp, _vp]),
     "cdx_mu_qkv_fwd": (ctypes.c_int, [_vp, _i64, _vp, _i64, _vp, _i64, _i64, _i32, _i32, _vp, _i64,
                                       _vp]),

@@ -287,10 +287,23 @@ class ComplexityAttention(nn.Module):
         handles head dims 32, 64 and 128 and H a multiple of 64)."""
         return self.head_dim in (32, 64, 128) and self.hidden_size % 64 == 0
 
+    def _out_proj(self, attn: torch.Tensor, residual: Optional[torch.Tensor]) -> torch.Tensor:
+        """o_proj(attn), or with ``residual``: residual + o_proj(attn) written into residual
+        (one GEMM with beta = 1, the block's residual add of core/layer.py:174)."""
+        if residual is None:
+            return self.o_proj(attn)
+        if residual.shape[:-1] != attn.shape[:-1] or not residual.is_contiguous():
+            raise ValueError("ComplexityAttention: residual must be contiguous and match the input rows")
+        residual.view(-1, residual.shape[-1]).addmm_(attn.reshape(-1, attn.shape[-1]), self.o_proj.weight.t())
+        return residual
+
     def forward(self, hidden_states: torch.Tensor, attention_mask: Optional[torch.Tensor] = None,
                 past_key_value: Optional[Tuple[torch.Tensor, torch.Tensor]] = None,
-                use_cache: bool = False, mu_prev: Optional[torch.Tensor] = None):
-        forward_only("ComplexityAttention", hidden_states, mu_prev, *self.parameters())
+                use_cache: bool = False, mu_prev: Optional[torch.Tensor] = None,
+                residual: Optional[torch.Tensor] = None):
+        """Returns (o_proj(attention), new_kv); with ``residual`` (the block input h,
+        contiguous) the output is added to it in place and residual is returned."""
+        forward_only("ComplexityAttention", hidden_states, mu_prev, residual, *self.parameters())
         B, S, _ = hidden_states.shape
         D = self.head_dim
         past_len = past_key_value[0].shape[2] if past_key_value is not None else 0
@@ -306,7 +319,7 @@ class ComplexityAttention(nn.Module):
             eps = self.q_norm.eps if self.use_qk_norm else 0.0
             q, k, vt = mu_qkv_rope(hidden_states, mu_prev, w, self.hidden_size, self.num_heads,
                                    self.num_kv_heads, D, qn[0], qn[1], eps, table, 0, v_transposed=True)
-            return self.o_proj(causal_attention(q, k, vt)), None
+            return self._out_proj(causal_attention(q, k, vt), residual), None
         if self.fused_prologue:
             # Projection, head split, QK RMSNorm and RoPE in one kernel (attention.py:120-155).
             w = self._cache.get(self)
@@ -345,7 +358,7 @@ class ComplexityAttention(nn.Module):
             dropout_p=self.attention_dropout if self.training else 0.0,
             is_causal=attention_mask is None)
         attn = attn.transpose(1, 2).contiguous().view(B, S, -1)
-        return self.o_proj(attn), new_kv
+        return self._out_proj(attn, residual), new_kv
 
 
 MuGuidedAttention = ComplexityAttention

@@ -21,7 +21,7 @@ from . import _native as nat
 from ._grad import forward_only
 from .attention import ComplexityAttention
 from .mlp import SwiGLU
-from .normalization import RMSNorm, add_rms_norm
+from .normalization import RMSNorm, add_rms_norm, rms_norm
 from .token_routed_mlp import RoutePlan, TokenRoutedMLP
 
 
@@ -103,10 +103,11 @@ class TransformerBlock(nn.Module):
         self.use_mu_guidance = use_mu_guidance
         self.mu_guidance = MuGuidance(hidden_size=hidden_size) if use_mu_guidance else None
 
-    def _mlp(self, x: torch.Tensor, token_ids, route: Optional[RoutePlan]) -> torch.Tensor:
+    def _mlp(self, x: torch.Tensor, token_ids, route: Optional[RoutePlan],
+             residual: Optional[torch.Tensor] = None) -> torch.Tensor:
         if self.use_token_routed_mlp:
-            return self.mlp(x, token_ids=token_ids, route=route)
-        return self.mlp(x)
+            return self.mlp(x, token_ids=token_ids, route=route, residual=residual)
+        return self.mlp(x, residual=residual)
 
     def forward(self, hidden_states: torch.Tensor, attention_mask: Optional[torch.Tensor] = None,
                 past_key_value: Optional[Tuple[torch.Tensor, torch.Tensor]] = None,
@@ -128,16 +129,19 @@ class TransformerBlock(nn.Module):
                       want_mu: bool = True):
         """One block given h (updated in place) and normed = input_layernorm(h).
 
-        Returns (h, next_norm(h_out), new_kv, mu) where the residual add after the MLP
-        is fused with ``next_norm`` and mu is already clamped to [-2, 2], the model's
-        clamp between layers (modeling.py:199-200).  ``want_mu=False`` skips mu for the
-        last layer, whose mu the reference computes and then discards."""
-        attn_out, new_kv = self.self_attn(normed, attention_mask=attention_mask,
-                                          past_key_value=past_key_value, use_cache=use_cache,
-                                          mu_prev=mu_prev)
+        Returns (h, next_norm(h_out), new_kv, mu) where mu is already clamped to [-2, 2],
+        the model's clamp between layers (modeling.py:199-200).  Both residual adds
+        (core/layer.py:174, 183) happen inside the kernels that produce the branch
+        outputs: o_proj as a GEMM with beta = 1, the MoE down pass in its scatter
+        epilogue; the norms that follow read h alone.  ``want_mu=False`` skips mu for
+        the last layer, whose mu the reference computes and then discards."""
+        if not h.is_contiguous():
+            raise ValueError("forward_fused: h must be contiguous (it is updated in place)")
+        _, new_kv = self.self_attn(normed, attention_mask=attention_mask, past_key_value=past_key_value,
+                                   use_cache=use_cache, mu_prev=mu_prev, residual=h)
         ln = self.post_attention_layernorm
-        normed, _ = add_rms_norm(attn_out, h, ln.weight, ln.eps, residual_out=h)
-        mlp_out = self._mlp(normed, token_ids, route)
-        normed, _ = add_rms_norm(mlp_out, h, next_norm.weight, next_norm.eps, residual_out=h)
+        normed = rms_norm(h, ln.weight, ln.eps)
+        self._mlp(normed, token_ids, route, residual=h)
+        normed = rms_norm(h, next_norm.weight, next_norm.eps)
         mu = self.mu_guidance.fused(h, -2.0, 2.0) if (want_mu and self.mu_guidance is not None) else None
         return h, normed, new_kv, mu

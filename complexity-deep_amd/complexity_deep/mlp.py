@@ -7,6 +7,8 @@ routing plan, so the dense configuration also stays on MFMA.
 
 from __future__ import annotations
 
+from typing import Optional
+
 import torch
 import torch.nn as nn
 
@@ -33,8 +35,10 @@ class SwiGLU(nn.Module):
         self._key = None
         self._packed = None
 
-    def forward(self, x: torch.Tensor) -> torch.Tensor:
-        forward_only("SwiGLU", x, *self.parameters())
+    def forward(self, x: torch.Tensor, residual: Optional[torch.Tensor] = None) -> torch.Tensor:
+        """``residual`` (same shape, contiguous) receives residual + MLP(x) in place and is
+        returned (the block's residual add fused into the down pass)."""
+        forward_only("SwiGLU", x, residual, *self.parameters())
         nat.require_device(x, what="SwiGLU")
         ws = (self.gate_proj.weight, self.up_proj.weight, self.down_proj.weight)
         key = tuple((w.data_ptr(), w._version, w.dtype, w.device) for w in ws)
@@ -46,6 +50,11 @@ class SwiGLU(nn.Module):
             self._key = key
         shape = x.shape
         x2d = x.reshape(-1, shape[-1]).contiguous()
+        r2d = None
+        if residual is not None:
+            if residual.shape != shape or not residual.is_contiguous():
+                raise ValueError("SwiGLU: residual must be a contiguous tensor shaped like the input")
+            r2d = residual.view(-1, shape[-1])
         out = moe_swiglu(x2d, identity_plan(x2d.shape[0], x.device), *self._packed,
-                         self.gate_proj.weight.shape[0], False)
+                         self.gate_proj.weight.shape[0], False, residual=r2d)
         return out.view(shape)

@@ -184,21 +184,29 @@ def pack_moe_weights(gate_w: torch.Tensor, up_w: torch.Tensor, down_w: torch.Ten
 
 
 def moe_swiglu(x2d: torch.Tensor, plan: RoutePlan, w_gu: torch.Tensor, w_down: torch.Tensor,
-               ie: int, has_shared: bool) -> torch.Tensor:
-    """out[T, H] = shared(x) + expert_e(x) through cdx_moe_swiglu_fwd."""
+               ie: int, has_shared: bool, residual: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """out[T, H] = shared(x) + expert_e(x) through cdx_moe_swiglu_fwd.
+
+    With ``residual`` ([T, H], contiguous) the rows are added to it in place instead
+    (cdx_moe_swiglu_residual_fwd) and ``residual`` is returned."""
     T, H = x2d.shape
     E = plan.num_experts
     P = padded_width(ie)
     S = 2 if has_shared else 1
     if w_gu.shape != (E, 2 * S * P, H) or w_down.shape != (E, H, S * P):
         raise ValueError("moe_swiglu: packed weight shapes do not match the plan/hidden size")
-    out = torch.empty_like(x2d)
+    if residual is not None:
+        nat.require_device(residual, x2d, what="moe_swiglu residual")
+        if residual.shape != x2d.shape or not residual.is_contiguous():
+            raise ValueError(f"moe_swiglu: residual must be a contiguous {tuple(x2d.shape)} tensor")
+        out, fn, fname = residual, nat.lib().cdx_moe_swiglu_residual_fwd, "cdx_moe_swiglu_residual_fwd"
+    else:
+        out, fn, fname = torch.empty_like(x2d), nat.lib().cdx_moe_swiglu_fwd, "cdx_moe_swiglu_fwd"
     inter = torch.empty(T, S * P, dtype=x2d.dtype, device=x2d.device)
     with nat.launch_region("moe_swiglu", x2d.device, T=T, H=H, Ie=ie, E=E, shared=has_shared):
-        nat.check(nat.lib().cdx_moe_swiglu_fwd(x2d.data_ptr(), T, H, ie, E, int(has_shared),
-                                               plan.perm.data_ptr(), plan.offsets.data_ptr(),
-                                               w_gu.data_ptr(), w_down.data_ptr(), inter.data_ptr(),
-                                               out.data_ptr(), nat.stream_of(x2d)), "cdx_moe_swiglu_fwd")
+        nat.check(fn(x2d.data_ptr(), T, H, ie, E, int(has_shared), plan.perm.data_ptr(), plan.offsets.data_ptr(),
+                     w_gu.data_ptr(), w_down.data_ptr(), inter.data_ptr(), out.data_ptr(), nat.stream_of(x2d)),
+                  fname)
     return out
 
 
@@ -271,25 +279,34 @@ class TokenRoutedMLP(nn.Module):
         return route_plan(token_ids, self.token_to_expert, self.num_experts)
 
     def forward(self, hidden_states: torch.Tensor, token_ids: Optional[torch.Tensor] = None,
-                route: Optional[RoutePlan] = None) -> torch.Tensor:
+                route: Optional[RoutePlan] = None, residual: Optional[torch.Tensor] = None) -> torch.Tensor:
         """[B, S, H] -> [B, S, H] = SharedMLP(x) + Expert_{map[token_id]}(x).
 
         ``route`` lets the caller pass a plan computed once for several layers that
-        share token ids and map (ComplexityModel does this)."""
-        forward_only("TokenRoutedMLP", hidden_states, *self.parameters())
+        share token ids and map (ComplexityModel does this).  ``residual`` (same shape,
+        contiguous) receives residual + MLP(x) in place and is returned: the block's
+        residual add (core/layer.py:183) fused into the down pass."""
+        forward_only("TokenRoutedMLP", hidden_states, residual, *self.parameters())
         nat.require_device(hidden_states, what="TokenRoutedMLP")
         shape = hidden_states.shape
         H = shape[-1]
         x2d = hidden_states.reshape(-1, H)
         x2d = x2d if x2d.is_contiguous() else x2d.contiguous()
         if token_ids is None and route is None:
-            return self._forward_all_experts(x2d).view(shape)
+            out = self._forward_all_experts(x2d).view(shape)
+            return out if residual is None else residual.add_(out)
         if route is None:
             route = self.plan(token_ids)
         if route.num_tokens != x2d.shape[0]:
             raise ValueError(f"TokenRoutedMLP: plan has {route.num_tokens} tokens, input has {x2d.shape[0]}")
         w_gu, w_down = self.packed_weights()
-        out = moe_swiglu(x2d, route, w_gu, w_down, self.expert_intermediate_size, self.use_shared_expert)
+        r2d = None
+        if residual is not None:
+            if residual.shape != shape or not residual.is_contiguous():
+                raise ValueError("TokenRoutedMLP: residual must be a contiguous tensor shaped like the input")
+            r2d = residual.view(-1, H)
+        out = moe_swiglu(x2d, route, w_gu, w_down, self.expert_intermediate_size, self.use_shared_expert,
+                         residual=r2d)
         return out.view(shape)
 
     def _forward_all_experts(self, x2d: torch.Tensor) -> torch.Tensor:

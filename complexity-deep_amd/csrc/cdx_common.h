@@ -42,6 +42,18 @@ __device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
 
 // 16-byte store with the non-temporal hint (streamed output that the kernel does
 // not read back).
+// Eight bf16 sums a + b, each added in fp32 and rounded once (a bf16 tensor add).
+__device__ __forceinline__ uint4 add_bf16x8(const uint4& a, const uint4& b) {
+  const uint32_t aw[4] = {a.x, a.y, a.z, a.w}, bw[4] = {b.x, b.y, b.z, b.w};
+  uint32_t r[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const float lo = __uint_as_float(aw[i] << 16) + __uint_as_float(bw[i] << 16);
+    const float hi = __uint_as_float(aw[i] & 0xFFFF0000u) + __uint_as_float(bw[i] & 0xFFFF0000u);
+    r[i] = pack_bf16x2(lo, hi);
+  }
+  return make_uint4(r[0], r[1], r[2], r[3]);
+}
 __device__ __forceinline__ void store_nt16(void* p, const uint4& v) {
   typedef __attribute__((ext_vector_type(4))) unsigned int u32x4_t;
   const u32x4_t w = {v.x, v.y, v.z, v.w};

@@ -44,7 +44,9 @@
 namespace cdx {
 
 enum class ALoad { kDense, kConcat, kGather };
-enum class Epi { kStore, kSwiGLU, kScatter, kQKRope, kBiasClamp };
+// kScatterAdd: like kScatter, but the scattered rows are added to what C holds (the
+// caller's residual stream, updated in place) with one bf16 rounding of the sum.
+enum class Epi { kStore, kSwiGLU, kScatter, kQKRope, kBiasClamp, kScatterAdd };
 
 // Parameters of the kQKRope epilogue (mu-QKV with QK RMSNorm and RoPE fused): the
 // packed [M, (nq + 2 nkv) * HD] projection is never stored; q, k and v go straight
@@ -677,6 +679,25 @@ __global__ __launch_bounds__(kGemmThreads, Cfg::MINB) void gemm_nt_kernel(const 
   // in order; the wait also keeps the compiler from reordering them).  The outputs
   // are streamed (non-temporal stores), which keeps the operands' panels in L2.
   __builtin_amdgcn_s_waitcnt(waitcnt_imm(63, 0));
+  // kScatterAdd: every residual piece this lane adds to is loaded up front, once the
+  // accumulators are staged and their registers free (loads interleaved with the
+  // stores below would wait one by one: a store may alias a later row's load).
+  constexpr int NIT = WM / RPI;  // store-loop iterations per lane
+  uint4 resid[EP == Epi::kScatterAdd ? NIT : 1];
+  if constexpr (EP == Epi::kScatterAdd) {
+    // Rows past the segment and columns past N read a clamped, valid piece (never
+    // stored): guarded loads would become branches, each waiting for its load.
+    const int jc = lane % OUT_CH;
+    const int n = min(n0 + wn * WN + jc * 8, p.N - 8);
+    int32_t prow[NIT];
+#pragma unroll
+    for (int i = 0; i < NIT; ++i) {
+      const int64_t gm = m0 + wm * WM + i * RPI + lane / OUT_CH;
+      prow[i] = p.perm[gm < m_end ? gm : m_end - 1];
+    }
+#pragma unroll
+    for (int i = 0; i < NIT; ++i) resid[i] = *reinterpret_cast<const uint4*>(p.c + (int64_t)prow[i] * p.ldc + n);
+  }
   if constexpr (EP == Epi::kQKRope) {
     if (vt_fast) {
       // V^T rows: 16 lanes per 256-byte row, four rows per instruction.
@@ -697,11 +718,10 @@ __global__ __launch_bounds__(kGemmThreads, Cfg::MINB) void gemm_nt_kernel(const 
     }
   }
   const int jc = lane % OUT_CH;  // this lane's chunk of a row
-#pragma unroll 4
-  for (int i = 0; i < WM / RPI; ++i) {
+  auto store_row = [&](int i) __attribute__((always_inline)) {
     const int r = i * RPI + lane / OUT_CH;
     const int64_t gm = m0 + wm * WM + r;
-    if (gm >= m_end) continue;
+    if (gm >= m_end) return;
     const uint4 v = *reinterpret_cast<const uint4*>(ep + r * OUT_ROWB + ((jc ^ (r % OUT_CH)) << 4));
     const int col = jc * 8;  // first output column of the chunk within the wave
     uint16_t* dst;
@@ -709,9 +729,9 @@ __global__ __launch_bounds__(kGemmThreads, Cfg::MINB) void gemm_nt_kernel(const 
       const QKRopeParams& q = p.qk;
       const int qd = q.nq * HD, kvd = q.nkv * HD;
       const int c0 = n0 + wn * WN + (col / HD) * HD;
-      if (c0 >= p.N) continue;
+      if (c0 >= p.N) return;
       const int kind = c0 < qd ? 0 : (c0 < qd + kvd ? 1 : 2);
-      if (kind == 2 && q.vt_ld > 0) continue;  // stored directly above
+      if (kind == 2 && q.vt_ld > 0) return;  // stored directly above
       const int head = kind == 0 ? c0 / HD : (kind == 1 ? (c0 - qd) / HD : (c0 - qd - kvd) / HD);
       const int nheads = kind == 0 ? q.nq : q.nkv;
       uint16_t* obase = kind == 0 ? q.q_out : (kind == 1 ? q.k_out : q.v_out);
@@ -721,15 +741,28 @@ __global__ __launch_bounds__(kGemmThreads, Cfg::MINB) void gemm_nt_kernel(const 
       dst = obase + ((b * nheads + head) * q.S + s) * HD + (col % HD);
     } else if constexpr (EP == Epi::kSwiGLU) {
       const int n = (n0 + wn * WN) / 2 + col;
-      if (2 * n >= p.N) continue;
+      if (2 * n >= p.N) return;
       dst = p.c + gm * p.ldc + n;
     } else {
       const int n = n0 + wn * WN + col;
-      if (n >= p.N) continue;
-      const int64_t orow = EP == Epi::kScatter ? (int64_t)p.perm[gm] : gm;
+      if (n >= p.N) return;
+      const int64_t orow = (EP == Epi::kScatter || EP == Epi::kScatterAdd) ? (int64_t)p.perm[gm] : gm;
       dst = p.c + orow * p.ldc + n;
     }
-    store_nt16(dst, v);
+    if constexpr (EP == Epi::kScatterAdd) {
+      // Each output row belongs to one tile and each 16-byte piece to one lane, so the
+      // read-add-write has no other writer.
+      store_nt16(dst, add_bf16x8(v, resid[i]));
+    } else {
+      store_nt16(dst, v);
+    }
+  };
+  if constexpr (EP == Epi::kScatterAdd) {
+#pragma unroll
+    for (int i = 0; i < NIT; ++i) store_row(i);  // resid[] is indexed by constants only
+  } else {
+#pragma unroll 4
+    for (int i = 0; i < NIT; ++i) store_row(i);
   }
 }
 

@@ -4,6 +4,8 @@
 //                        epilogue, writing head-major q, k, v
 //   cdx_moe_swiglu_fwd   piece 1b: gather + gate/up + SwiGLU, then down + scatter,
 //                        with the shared expert folded into both passes
+//   cdx_moe_swiglu_residual_fwd  the same, the scattered rows added to the residual
+//                        stream in place (the block's h = h + mlp(x))
 //   cdx_grouped_gemm_fwd plain grouped GEMM over expert segments
 //   cdx_mu_guidance_fwd  mu = clamp(h @ W_mu^T + clamp(mu_param), lo, hi), the
 //                        producer of the next layer's mu operand
@@ -77,13 +79,14 @@ extern "C" int cdx_mu_qkv_fwd(const uint16_t* x, int64_t ldx, const uint16_t* mu
   return launch<ALoad::kDense, Epi::kStore>(p, s, name);
 }
 
-extern "C" int cdx_moe_swiglu_fwd(const uint16_t* x, int64_t T, int32_t H, int32_t Ie, int32_t E,
-                                  int32_t has_shared, const int32_t* perm, const int32_t* offsets,
-                                  const uint16_t* w_gu, const uint16_t* w_down, uint16_t* inter,
-                                  uint16_t* out, void* stream) {
-  using namespace cdx;
+namespace cdx {
+namespace {
+
+// Both MoE passes; with `residual`, the down pass adds its rows to `out` in place.
+int moe_swiglu(const uint16_t* x, int64_t T, int32_t H, int32_t Ie, int32_t E, int32_t has_shared,
+               const int32_t* perm, const int32_t* offsets, const uint16_t* w_gu, const uint16_t* w_down,
+               uint16_t* inter, uint16_t* out, void* stream, bool residual, const char* name) {
   clear_error();
-  const char* name = "cdx_moe_swiglu_fwd";
   if (T < 0 || T > INT32_MAX || H <= 0 || Ie <= 0 || E <= 0 || E > 64)
     return fail(CDX_EINVAL, "%s: bad shape T=%lld H=%d Ie=%d E=%d", name, (long long)T, H, Ie, E);
   if (H % 64 != 0) return fail(CDX_EUNSUPPORTED, "%s: H=%d must be a multiple of 64", name, H);
@@ -137,7 +140,27 @@ extern "C" int cdx_moe_swiglu_fwd(const uint16_t* x, int64_t T, int32_t H, int32
   p2.c = out;
   p2.ldc = H;
   p2.mt_count = mt;
+  if (residual) return launch<ALoad::kDense, Epi::kScatterAdd>(p2, s, name);
   return launch<ALoad::kDense, Epi::kScatter>(p2, s, name);
+}
+
+}  // namespace
+}  // namespace cdx
+
+extern "C" int cdx_moe_swiglu_fwd(const uint16_t* x, int64_t T, int32_t H, int32_t Ie, int32_t E,
+                                  int32_t has_shared, const int32_t* perm, const int32_t* offsets,
+                                  const uint16_t* w_gu, const uint16_t* w_down, uint16_t* inter,
+                                  uint16_t* out, void* stream) {
+  return cdx::moe_swiglu(x, T, H, Ie, E, has_shared, perm, offsets, w_gu, w_down, inter, out, stream, false,
+                         "cdx_moe_swiglu_fwd");
+}
+
+extern "C" int cdx_moe_swiglu_residual_fwd(const uint16_t* x, int64_t T, int32_t H, int32_t Ie, int32_t E,
+                                           int32_t has_shared, const int32_t* perm, const int32_t* offsets,
+                                           const uint16_t* w_gu, const uint16_t* w_down, uint16_t* inter,
+                                           uint16_t* residual, void* stream) {
+  return cdx::moe_swiglu(x, T, H, Ie, E, has_shared, perm, offsets, w_gu, w_down, inter, residual, stream, true,
+                         "cdx_moe_swiglu_residual_fwd");
 }
 
 extern "C" int cdx_grouped_gemm_fwd(const uint16_t* a, int64_t T, int32_t K, int32_t N, int32_t E,

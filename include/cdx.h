@@ -140,6 +140,21 @@ int cdx_moe_swiglu_fwd(const uint16_t* x_dev, int64_t T, int32_t H, int32_t Ie, 
                        void* stream);
 
 /*
+ * cdx_moe_swiglu_fwd with the block's residual add fused into the down pass:
+ *   residual[t, :] = residual[t, :] + (shared(x) + expert_{e(t)}(x))[t, :]
+ * in place, the MLP rows rounded to bf16 and then added with one more bf16 rounding
+ * (the same two roundings as the reference's bf16 `residual + hidden_states`).
+ * Arguments as cdx_moe_swiglu_fwd, with residual_dev [T, H] in place of out_dev.
+ * Replaces: core/layer.py:176-183 (residual = h; h = mlp(norm(h)); h = residual + h),
+ * the MLP half of the block.
+ */
+int cdx_moe_swiglu_residual_fwd(const uint16_t* x_dev, int64_t T, int32_t H, int32_t Ie, int32_t E,
+                                int32_t has_shared, const int32_t* perm_dev,
+                                const int32_t* offsets_dev, const uint16_t* w_gu_dev,
+                                const uint16_t* w_down_dev, uint16_t* inter_dev,
+                                uint16_t* residual_dev, void* stream);
+
+/*
  * Grouped GEMM over expert segments of an already sorted token matrix:
  *   out[offsets[e]:offsets[e+1], :] = a[offsets[e]:offsets[e+1], :] @ W[e]
  * with W given K-contiguous: w_dev is [E][N][K] (W[e] transposed).  K % 64 == 0.

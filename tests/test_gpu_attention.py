@@ -97,3 +97,27 @@ def test_attention_module_matches_sdpa_path(cdx, monkeypatch, H, nq, nkv, S):
     d = (fused.float() - ref.float()).abs().max() / ref.float().abs().max()
     print("max rel kernel vs SDPA path", float(d), flush=True)
     assert float(d) < 3e-2
+
+
+def test_attention_residual_out_projection(cdx):
+    """ComplexityAttention with ``residual``: o_proj and the block's residual add
+    (core/layer.py:174) as one GEMM with beta = 1, written into the residual, against
+    o_proj followed by the bf16 add (one rounding fewer, so bf16 tolerance)."""
+    print("attention residual o_proj", flush=True)
+    torch.manual_seed(11)
+    H, nq, nkv, S = 1024, 8, 4, 130
+    attn = cdx.ComplexityAttention(H, nq, nkv).to(bf16).cuda().eval()
+    with torch.no_grad():
+        for lin in (attn.q_proj, attn.k_proj, attn.v_proj, attn.mu_to_q, attn.mu_to_k, attn.mu_to_v, attn.o_proj):
+            lin.weight.normal_(0, 0.02)
+    x = torch.randn(2, S, H, device="cuda").to(bf16)
+    mu = torch.randn(2, S, H, device="cuda").clamp(-2, 2).to(bf16)
+    h = torch.randn(2, S, H, device="cuda").to(bf16)
+    with torch.no_grad():
+        out, _ = attn(x, mu_prev=mu)
+        expect = h + out
+        got = h.clone()
+        ret, kv = attn(x, mu_prev=mu, residual=got)
+    torch.cuda.synchronize()
+    assert ret.data_ptr() == got.data_ptr() and kv is None
+    assert_close_bf16(got, expect.float(), "attention + residual")

@@ -129,3 +129,46 @@ def test_grouped_gemm_api(cdx, oracle):
     out = cdx.cggr_grouped_gemm(a.cuda(), w.cuda(), offs.cuda())
     ref = oracle.grouped_gemm(a.float(), w.float(), offs.numpy())
     assert_close_bf16(out, ref, "grouped gemm")
+
+
+@pytest.mark.parametrize("T,H,I,E,shared", [(16384, 2048, 5632, 8, True), (300, 512, 1408, 4, False)])
+def test_moe_residual_add_matches_separate_add(cdx, T, H, I, E, shared):
+    """cdx_moe_swiglu_residual_fwd (the block's h + mlp(x), core/layer.py:183, fused
+    into the down pass) against the plain kernel followed by a bf16 add: the fused
+    epilogue rounds the MLP rows to bf16 and then the sum, exactly like the tensor
+    add, so the two agree bit for bit."""
+    from complexity_deep import synthetic as syn
+    print(f"moe residual T={T} H={H} E={E}", flush=True)
+    tmap = syn.binpacked_map(32000, E)
+    m = _module(cdx, H, I, E, 32000, shared, 5, tmap)
+    ids = syn.zipf_token_ids(1, T, 32000, seed=2).cuda()
+    x = syn.normal_bf16((1, T, H), seed=3).cuda()
+    r = syn.normal_bf16((1, T, H), seed=4).cuda()
+    with torch.no_grad():
+        expect = r + m(x, token_ids=ids)
+        got = r.clone()
+        out = m(x, token_ids=ids, residual=got)
+    torch.cuda.synchronize()
+    assert out.data_ptr() == got.data_ptr()
+    assert torch.equal(got, expect)
+
+
+def test_dense_swiglu_and_average_path_residual(cdx):
+    """The residual form of the dense SwiGLU (E = 1 through the same kernels) and of
+    the token_ids=None average path."""
+    print("dense / average residual", flush=True)
+    torch.manual_seed(7)
+    d = cdx.SwiGLU(256, 704).to(bf16).cuda()
+    x = torch.randn(1, 96, 256, device="cuda").to(bf16)
+    r = torch.randn(1, 96, 256, device="cuda").to(bf16)
+    with torch.no_grad():
+        expect = r + d(x)
+        got = r.clone()
+        d(x, residual=got)
+    assert torch.equal(got, expect)
+    m = _module(cdx, 256, 704, 4, 1000, True, 8)
+    with torch.no_grad():
+        expect = r + m(x)
+        got = r.clone()
+        m(x, residual=got)
+    assert torch.equal(got, expect)
