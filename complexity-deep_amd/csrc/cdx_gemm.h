@@ -43,7 +43,12 @@
 
 namespace cdx {
 
-enum class ALoad { kDense, kConcat, kGather };
+// kSegmented (the MoE down pass): M tiles of kBM consecutive sorted rows regardless of
+// the expert segments (offsets); a tile runs the shared K columns [0, k_split) once
+// for all its rows, then the expert columns [k_split, K) once per expert it touches,
+// with that expert's B and the other experts' A rows read as zeros.  No tile is
+// padded to an expert boundary, so the grid holds ceil(M / kBM) M tiles.
+enum class ALoad { kDense, kConcat, kGather, kSegmented };
 // kScatterAdd: like kScatter, but the scattered rows are added to what C holds (the
 // caller's residual stream, updated in place) with one bf16 rounding of the sum.
 enum class Epi { kStore, kSwiGLU, kScatter, kQKRope, kBiasClamp, kScatterAdd };
@@ -213,7 +218,7 @@ __global__ __launch_bounds__(kGemmThreads, Cfg::MINB) void gemm_nt_kernel(const 
   // segment offsets, so that the surplus blocks neither take an XCD's share nor sit
   // in the middle of the logical order.
   int mt_real = p.mt_count;
-  if (p.offsets != nullptr) {
+  if (AL != ALoad::kSegmented && p.offsets != nullptr) {
     mt_real = 0;
     for (int x = 0; x < p.E; ++x) mt_real += (p.offsets[x + 1] - p.offsets[x] + kBM - 1) / kBM;
     mt_real = min(mt_real, p.mt_count);
@@ -225,12 +230,27 @@ __global__ __launch_bounds__(kGemmThreads, Cfg::MINB) void gemm_nt_kernel(const 
   const int first_m = group * kGroupM;
   const int gsz = min(mt_real - first_m, kGroupM);
   const int in_group = L - group * per_group;
-  const int mt = first_m + in_group % gsz;
-  const int nt = in_group / gsz;
+  // The divisions above run on the vector unit; pinning the tile indices to scalar
+  // registers keeps every descriptor built from them scalar (a descriptor operand in
+  // vector registers turns each DMA into a loop over lanes).
+  const int mt = __builtin_amdgcn_readfirstlane(first_m + in_group % gsz);
+  const int nt = __builtin_amdgcn_readfirstlane(in_group / gsz);
 
   int64_t m0, m_end;
   int e = 0;
-  if (p.offsets != nullptr) {
+  int e_lo = 0, n_exp = 1;  // kSegmented: first expert of the tile, experts it touches
+  if constexpr (AL == ALoad::kSegmented) {
+    m0 = (int64_t)mt * kBM;
+    m_end = min(p.M, m0 + kBM);
+    if (m0 >= m_end) return;
+    // Experts holding rows m0 and m_end - 1 (segments are consecutive and sorted).
+    int e_hi = 0;
+    for (int x = 0; x < p.E; ++x) {
+      if (p.offsets[x] <= m0 && m0 < p.offsets[x + 1]) e_lo = x;
+      if (p.offsets[x] <= m_end - 1 && m_end - 1 < p.offsets[x + 1]) e_hi = x;
+    }
+    n_exp = e_hi - e_lo + 1;
+  } else if (p.offsets != nullptr) {
     int before = 0;
     e = -1;
     for (int x = 0; x < p.E; ++x) {
@@ -273,14 +293,28 @@ __global__ __launch_bounds__(kGemmThreads, Cfg::MINB) void gemm_nt_kernel(const 
   const uintptr_t a_base = (uintptr_t)(AL == ALoad::kGather ? p.a : p.a + m0 * p.lda);
   const uintptr_t a2_base =
       AL == ALoad::kConcat ? (uintptr_t)(p.a2 + m0 * p.lda2) - (uintptr_t)p.k_split * 2 : a_base;
-  const __amdgpu_buffer_rsrc_t rs_a = make_rsrc((const void*)a_base);
+  // kSegmented: the A descriptor covers the tile's rows only, so that a masked row's
+  // offset (kMaskedOff) reads zeros; each row remembers its expert (-1 past m_end).
+  const __amdgpu_buffer_rsrc_t rs_a =
+      AL == ALoad::kSegmented ? make_rsrc((const void*)a_base, (uint32_t)((m_end - m0) * p.lda * 2))
+                              : make_rsrc((const void*)a_base);
   const __amdgpu_buffer_rsrc_t rs_b = make_rsrc(bexp + (int64_t)n0 * p.ldb);
+  constexpr uint32_t kMaskedOff = 0x80000000u;
   uint32_t a_off[LD_A], a2_off[LD_A], b_off[LD_B];
+  int a_exp[AL == ALoad::kSegmented ? LD_A : 1];
 #pragma unroll
   for (int j = 0; j < LD_A; ++j) {
     const int r = wave * (kBM / 4) + j * ROWS_PER_DMA + dr;
     const int dchunk = (lane % CPR) ^ ((r / RPL) % CPR);
     int64_t gm = m0 + r;
+    if constexpr (AL == ALoad::kSegmented) {
+      int ex = -1;
+      if (gm < m_end) {
+        ex = e_lo;
+        for (int x = e_lo + 1; x < e_lo + n_exp; ++x) ex += p.offsets[x] <= gm ? 1 : 0;
+      }
+      a_exp[j] = ex;
+    }
     gm = gm < m_end ? gm : m_end - 1;  // rows past the segment are loaded but never stored
     if (AL == ALoad::kGather) {
       a_off[j] = (uint32_t)(((int64_t)p.perm[gm] * p.lda + dchunk * 8) * 2);
@@ -300,30 +334,72 @@ __global__ __launch_bounds__(kGemmThreads, Cfg::MINB) void gemm_nt_kernel(const 
   const int a_dma_off = wave * (kBM / 4) * ROW_BYTES;  // this wave's first DMA block in A
   const int b_dma_off = A_TILE_BYTES + wave * (kBN / 4) * ROW_BYTES;
 
-  // One DMA instruction of step kt into `stage`: d < LD_A covers A rows, then B.
+  // Where K step kt reads: k0 = its first K column (the same for A and B), and for
+  // kSegmented the expert whose columns and B it is (-1: the shared columns).
   // Steps past the end (kt >= KT) go through the empty descriptor: the pipeline
   // issues the same instructions every step, and those fetch nothing.
-  const int KT = p.K / kBK;
+  const int ks0 = AL == ALoad::kSegmented ? p.k_split / kBK : 0;          // shared K steps
+  const int ks1 = AL == ALoad::kSegmented ? (p.K - p.k_split) / kBK : 1;  // K steps per expert
+  const int KT = AL == ALoad::kSegmented ? ks0 + n_exp * ks1 : p.K / kBK;
   const __amdgpu_buffer_rsrc_t rs_none = make_rsrc(p.b, 0u);
-  auto dma1 = [&](int kt, int stage, int d) __attribute__((always_inline)) {
-    const int k0 = kt * kBK;
-    const bool live = kt < KT;
+  struct StepSrc {
+    int k0;
+    int e;
+    bool live;
+  };
+  auto step_src = [&](int kt) __attribute__((always_inline)) { return StepSrc{kt * kBK, -1, kt < KT}; };
+  // kSegmented: the DMA steps are issued in order, so their sources advance by scalar
+  // selects instead of a division per step: the shared columns, then each expert's.
+  StepSrc seg_next{ks0 > 0 ? 0 : p.k_split, ks0 > 0 ? -1 : e_lo, true};
+  int seg_step = 0;
+  // B descriptor of the step's expert (the shared columns are packed with every
+  // expert's down weights; e_lo's serve), or the empty one past the end.
+  // Kept as an address, not as a descriptor: a loop-carried descriptor is not kept in
+  // scalar registers.
+  const uintptr_t b_estep = (uintptr_t)p.b_estride * 2;
+  uintptr_t seg_bptr = (uintptr_t)(p.b + (int64_t)n0 * p.ldb + (int64_t)e_lo * p.b_estride);
+  auto seg_advance = [&]() __attribute__((always_inline)) {
+    const int k1 = seg_next.k0 + kBK;
+    const bool shared = seg_next.e < 0;
+    const bool wrap = shared ? k1 >= p.k_split : k1 >= p.K;
+    const bool next_e = wrap && !shared;
+    seg_next.e = wrap ? (shared ? e_lo : seg_next.e + 1) : seg_next.e;
+    seg_next.k0 = wrap ? p.k_split : k1;
+    seg_bptr += next_e ? b_estep : 0;
+    ++seg_step;
+    seg_next.live = seg_step < KT;
+  };
+  (void)ks1;
+  // One DMA instruction of step st into `stage`: d < LD_A covers A rows, then B.
+  auto dma1 = [&](const StepSrc& st, int stage, int d) __attribute__((always_inline)) {
+    const int k0 = st.k0;
+    const bool live = st.live;
     uint8_t* dst = lds + stage * STAGE_BYTES;
     if (d < LD_A) {
       if constexpr (AL == ALoad::kConcat) {
         const bool second = k0 >= p.k_split;
         const __amdgpu_buffer_rsrc_t r = make_rsrc((const void*)(second ? a2_base : a_base));
         buf_dma16(live ? r : rs_none, second ? a2_off[d] : a_off[d], (uint32_t)k0 * 2, dst + a_dma_off + d * 1024);
+      } else if constexpr (AL == ALoad::kSegmented) {
+        const bool mine = st.e < 0 || a_exp[d] == st.e;
+        buf_dma16(live ? rs_a : rs_none, mine ? a_off[d] : kMaskedOff, (uint32_t)k0 * 2, dst + a_dma_off + d * 1024);
       } else {
         buf_dma16(live ? rs_a : rs_none, a_off[d], (uint32_t)k0 * 2, dst + a_dma_off + d * 1024);
       }
     } else {
-      buf_dma16(live ? rs_b : rs_none, b_off[d - LD_A], (uint32_t)k0 * 2, dst + b_dma_off + (d - LD_A) * 1024);
+      if constexpr (AL == ALoad::kSegmented) {
+        const __amdgpu_buffer_rsrc_t r = make_rsrc((const void*)seg_bptr);
+        buf_dma16(live ? r : rs_none, b_off[d - LD_A], (uint32_t)k0 * 2, dst + b_dma_off + (d - LD_A) * 1024);
+      } else {
+        buf_dma16(live ? rs_b : rs_none, b_off[d - LD_A], (uint32_t)k0 * 2, dst + b_dma_off + (d - LD_A) * 1024);
+      }
     }
   };
   auto issue = [&](int kt, int stage) __attribute__((always_inline)) {
+    const StepSrc st = AL == ALoad::kSegmented ? seg_next : step_src(kt);
 #pragma unroll
-    for (int d = 0; d < LD_PER_STEP; ++d) dma1(kt, stage, d);
+    for (int d = 0; d < LD_PER_STEP; ++d) dma1(st, stage, d);
+    if constexpr (AL == ALoad::kSegmented) seg_advance();
   };
 
   // ---- fragments -------------------------------------------------------------
@@ -389,6 +465,7 @@ __global__ __launch_bounds__(kGemmThreads, Cfg::MINB) void gemm_nt_kernel(const 
   // instructions (past the end they fetch nothing), so one vmcnt threshold serves
   // all steps.  The final step (last = true) only computes.
   auto last_substep = [&](int kt, int stage, int next_stage, bool last) __attribute__((always_inline)) {
+    const StepSrc st = AL == ALoad::kSegmented ? seg_next : step_src(kt + kStages);
     if (!last) {
       __builtin_amdgcn_s_waitcnt(waitcnt_imm(LD_PER_STEP * (kStages - 2), 0));
       __syncthreads();
@@ -397,13 +474,14 @@ __global__ __launch_bounds__(kGemmThreads, Cfg::MINB) void gemm_nt_kernel(const 
 #pragma unroll
     for (int i = 0; i < MI * NI; ++i) {
       mfma1((NSUB - 1) & 1, i);
-      if (!last && i % DMA_EVERY == DMA_OFF && i / DMA_EVERY < LD_PER_STEP) dma1(kt + kStages, stage, i / DMA_EVERY);
+      if (!last && i % DMA_EVERY == DMA_OFF && i / DMA_EVERY < LD_PER_STEP) dma1(st, stage, i / DMA_EVERY);
       if (!last && i % RD_EVERY == 0 && i / RD_EVERY < NFRAG) read1(next_stage, 0, 0, i / RD_EVERY);
       __builtin_amdgcn_sched_barrier(0);
     }
     if (!last) {
 #pragma unroll
-      for (int d = (MI * NI - DMA_OFF + DMA_EVERY - 1) / DMA_EVERY; d < LD_PER_STEP; ++d) dma1(kt + kStages, stage, d);
+      for (int d = (MI * NI - DMA_OFF + DMA_EVERY - 1) / DMA_EVERY; d < LD_PER_STEP; ++d) dma1(st, stage, d);
+      if constexpr (AL == ALoad::kSegmented) seg_advance();
     }
     __builtin_amdgcn_sched_barrier(0);
   };

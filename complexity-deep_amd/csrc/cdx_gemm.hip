@@ -124,10 +124,22 @@ int moe_swiglu(const uint16_t* x, int64_t T, int32_t H, int32_t Ie, int32_t E, i
   if (int rc = launch<ALoad::kGather, Epi::kSwiGLU>(p1, s, name)) return rc;
 
   // Pass 2: activations (sorted order) times [shared_down | down[e]], rows scattered back.
+  // Two tile layouts.  Per-expert tiles (as in pass 1) leave up to one partial tile per
+  // expert; tiles that ignore the expert boundaries (kSegmented) leave none, but a tile
+  // that spans experts runs the expert columns once per expert.  The kernel holds one
+  // block per CU, so price each in K steps per CU: whole rounds of tiles, plus one
+  // spanning tile's extra expert columns for kSegmented.  At the 1B shape (8 experts,
+  // 2048 columns) per-expert tiles take 2.2 rounds, i.e. 3 x 22 steps, the segmented
+  // ones 2 x 22 + 11.
+  const int64_t ks_shared = has_shared ? P / DefaultCfg::BK : 0, ks_expert = P / DefaultCfg::BK;
+  const int64_t nt2 = cdiv(H, DefaultCfg::BN), cus = device_cu_count();
+  const int64_t cost_expert = cdiv((cdiv(T, kBM) + E - 1) * nt2, cus) * (ks_shared + ks_expert);
+  const int64_t cost_segmented = cdiv(cdiv(T, kBM) * nt2, cus) * (ks_shared + ks_expert) + ks_expert;
+  const bool segmented = cost_segmented < cost_expert;
   GemmParams p2{};
   p2.a = inter;
   p2.lda = k_down;
-  p2.k_split = k_down;
+  p2.k_split = segmented ? (has_shared ? P : 0) : k_down;
   p2.perm = perm;
   p2.offsets = offsets;
   p2.E = E;
@@ -139,6 +151,11 @@ int moe_swiglu(const uint16_t* x, int64_t T, int32_t H, int32_t Ie, int32_t E, i
   p2.K = k_down;
   p2.c = out;
   p2.ldc = H;
+  if (segmented) {
+    p2.mt_count = (int32_t)cdiv(T, kBM);
+    if (residual) return launch<ALoad::kSegmented, Epi::kScatterAdd>(p2, s, name);
+    return launch<ALoad::kSegmented, Epi::kScatter>(p2, s, name);
+  }
   p2.mt_count = mt;
   if (residual) return launch<ALoad::kDense, Epi::kScatterAdd>(p2, s, name);
   return launch<ALoad::kDense, Epi::kScatter>(p2, s, name);

@@ -126,11 +126,7 @@ int launch_vpl(const uint16_t* x, const uint16_t* res, const uint16_t* w, float 
                int H, uint16_t* out, uint16_t* res_out, hipStream_t s) {
   // Four blocks (16 waves) per CU; each wave walks about T / waves rows, so that its
   // prefetch of the next row has work to hide behind.
-  int dev = 0, cus = 0;
-  if (hipGetDevice(&dev) != hipSuccess ||
-      hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0)
-    cus = 256;
-  const int64_t max_blocks = (int64_t)cus * 4;
+  const int64_t max_blocks = (int64_t)device_cu_count() * 4;
   const int64_t blocks = std::min<int64_t>((T + kWavesPerBlock - 1) / kWavesPerBlock, max_blocks);
   const dim3 grid((unsigned)blocks);
   const dim3 block(64 * kWavesPerBlock);

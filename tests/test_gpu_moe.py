@@ -8,6 +8,7 @@ brute force) on the same bf16 inputs and weights:
     every expert (outputs are per-row independent, so a row check is exact);
   * no shared expert, Ie needing padding (176 -> 192), E=1, an expert with no
     tokens, single tokens, the token_ids=None average path, the dense SwiGLU;
+  * shapes whose down pass runs M tiles that span experts (empty experts inside);
   * the grouped-GEMM operator API.
 """
 
@@ -96,6 +97,29 @@ def test_moe_ragged(cdx, oracle, T, H, I, E, shared, V):
     out = _run(m, x.view(1, T, H), ids.view(1, T).cuda())
     ref = _oracle(oracle, m, x.view(1, T, H), ids.view(1, T))
     assert_close_bf16(out, ref, "ragged")
+
+
+@pytest.mark.parametrize("T,H,I,E,shared,empty", [(777, 16384, 704, 4, True, (1,)),
+                                                  (1024, 16384, 1408, 8, False, (2, 3, 7))])
+def test_moe_down_tiles_across_experts(cdx, oracle, T, H, I, E, shared, empty):
+    """Shapes whose down pass takes the M tiles that ignore expert boundaries: 16384
+    output columns are 64 column tiles, so the up-to-one partial tile per expert would
+    cost a whole extra round of tiles on 256 CUs (T=777: 2 rounds x 6 K steps against
+    6 + 3; T=1024, no shared expert: 3 x 3 against 3 + 3).  Experts without tokens sit
+    inside tiles that span experts, and the last tile is partial."""
+    print(f"moe spanning tiles T={T} H={H} E={E} shared={shared} empty={empty}", flush=True)
+    g = torch.Generator().manual_seed(T)
+    live = torch.tensor([e for e in range(E) if e not in empty])
+    V = 1000
+    tmap = live[torch.randint(0, len(live), (V,), generator=g)]
+    m = _module(cdx, H, I, E, V, shared, T, tmap)
+    ids = torch.randint(-2, V + 2, (T,), generator=g)
+    # x / 4 keeps the gate/up sums over 16384 columns at the scale of the other cases
+    # (the absolute error bounds are set for outputs of unit scale).
+    x = (torch.randn(T, H, generator=g) * 0.25).to(bf16).cuda()
+    out = _run(m, x.view(1, T, H), ids.view(1, T).cuda())
+    ref = _oracle(oracle, m, x.view(1, T, H), ids.view(1, T))
+    assert_close_bf16(out, ref, "spanning tiles")
 
 
 def test_moe_average_all_experts(cdx, oracle):
