@@ -559,8 +559,17 @@ __global__ __launch_bounds__(kGemmThreads, Cfg::MINB) void gemm_nt_kernel(const 
     vt_fast = p.qk.vt_ld > 0 && n0 + wn * WN >= (p.qk.nq + p.qk.nkv) * HD && (tok_s0 & 15) == 0 &&
               (int64_t)tok_s0 + WM <= p.qk.S && m0 + wm * WM + WM <= m_end;
   }
+  // A wave whose WM rows lie in one sequence (every wave when S % WM == 0) needs no
+  // division per row.
+  bool one_seq = false;
+  if constexpr (EP == Epi::kQKRope) one_seq = (int64_t)tok_s0 + WM <= p.qk.S;
   auto tok = [&](int r, int64_t& b, uint32_t& s) __attribute__((always_inline)) {
     const uint32_t t = tok_s0 + (uint32_t)r, S32 = (uint32_t)p.qk.S;
+    if (one_seq) {
+      s = t;
+      b = tok_b0;
+      return;
+    }
     const uint32_t w = t / S32;
     s = t - w * S32;
     b = tok_b0 + w;
