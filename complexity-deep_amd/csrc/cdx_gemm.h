@@ -769,22 +769,25 @@ __global__ __launch_bounds__(kGemmThreads, Cfg::MINB) void gemm_nt_kernel(const 
   // in order; the wait also keeps the compiler from reordering them).  The outputs
   // are streamed (non-temporal stores), which keeps the operands' panels in L2.
   __builtin_amdgcn_s_waitcnt(waitcnt_imm(63, 0));
-  // kScatterAdd: every residual piece this lane adds to is loaded up front, once the
+  // Scatter epilogues: the output row of every store-loop iteration (perm) and, for
+  // kScatterAdd, every residual piece this lane adds to are loaded up front, once the
   // accumulators are staged and their registers free (loads interleaved with the
   // stores below would wait one by one: a store may alias a later row's load).
+  // Rows past the segment and columns past N read a clamped, valid piece (never
+  // stored): guarded loads would become branches, each waiting for its load.
   constexpr int NIT = WM / RPI;  // store-loop iterations per lane
+  constexpr bool kScatterRows = EP == Epi::kScatter || EP == Epi::kScatterAdd;
+  int32_t prow[kScatterRows ? NIT : 1];
   uint4 resid[EP == Epi::kScatterAdd ? NIT : 1];
-  if constexpr (EP == Epi::kScatterAdd) {
-    // Rows past the segment and columns past N read a clamped, valid piece (never
-    // stored): guarded loads would become branches, each waiting for its load.
-    const int jc = lane % OUT_CH;
-    const int n = min(n0 + wn * WN + jc * 8, p.N - 8);
-    int32_t prow[NIT];
+  if constexpr (kScatterRows) {
 #pragma unroll
     for (int i = 0; i < NIT; ++i) {
       const int64_t gm = m0 + wm * WM + i * RPI + lane / OUT_CH;
       prow[i] = p.perm[gm < m_end ? gm : m_end - 1];
     }
+  }
+  if constexpr (EP == Epi::kScatterAdd) {
+    const int n = min(n0 + wn * WN + (lane % OUT_CH) * 8, p.N - 8);
 #pragma unroll
     for (int i = 0; i < NIT; ++i) resid[i] = *reinterpret_cast<const uint4*>(p.c + (int64_t)prow[i] * p.ldc + n);
   }
@@ -836,7 +839,8 @@ __global__ __launch_bounds__(kGemmThreads, Cfg::MINB) void gemm_nt_kernel(const 
     } else {
       const int n = n0 + wn * WN + col;
       if (n >= p.N) return;
-      const int64_t orow = (EP == Epi::kScatter || EP == Epi::kScatterAdd) ? (int64_t)p.perm[gm] : gm;
+      int64_t orow = gm;
+      if constexpr (kScatterRows) orow = prow[i];
       dst = p.c + orow * p.ldc + n;
     }
     if constexpr (EP == Epi::kScatterAdd) {
@@ -847,9 +851,9 @@ __global__ __launch_bounds__(kGemmThreads, Cfg::MINB) void gemm_nt_kernel(const 
       store_nt16(dst, v);
     }
   };
-  if constexpr (EP == Epi::kScatterAdd) {
+  if constexpr (kScatterRows) {
 #pragma unroll
-    for (int i = 0; i < NIT; ++i) store_row(i);  // resid[] is indexed by constants only
+    for (int i = 0; i < NIT; ++i) store_row(i);  // prow[] and resid[] are indexed by constants only
   } else {
 #pragma unroll 4
     for (int i = 0; i < NIT; ++i) store_row(i);
