@@ -372,7 +372,6 @@ __global__ __launch_bounds__(kGemmThreads, Cfg::MINB) void gemm_nt_kernel(const 
     ++seg_step;
     seg_next.live = seg_step < KT;
   };
-  (void)ks1;
   // One DMA instruction of step st into `stage`: d < LD_A covers A rows, then B.
   auto dma1 = [&](const StepSrc& st, int stage, int d) __attribute__((always_inline)) {
     const int k0 = st.k0;
