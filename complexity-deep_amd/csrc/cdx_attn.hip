@@ -359,9 +359,16 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_kernel(const AttnParams p) {
   for (; t < nt; ++t) sync(t, t & 1);
 
   // ---- O = O^T / l -> out[b, m, h * HD + d] ----------------------------------------
-  if (m >= S) return;
-  const float inv_l = 1.f / l_run;
-  uint16_t* orow = p.out + ((int64_t)b * S + m) * ((int64_t)p.nq * HD) + (int64_t)h * HD;
+  // A lane holds 8-byte pieces of one query row, so direct stores would write 16-byte
+  // runs of 32 rows per instruction.  The rows are staged through the K buffers
+  // instead (free once every wave is past its last tile; 32 rows of HD values per
+  // wave fill them exactly), 16-byte chunk c of row r at position c ^ (r % OCH), and
+  // go out as whole HD * 2-byte rows.
+  constexpr int OROWB = HD * 2, OCH = OROWB / 16, ORPI = 64 / OCH;
+  static_assert(4 * 32 * OROWB <= 2 * K_BYTES, "output staging must fit the K buffers");
+  __syncthreads();
+  uint8_t* ost = lds + wave * 32 * OROWB;
+  const float inv_l = 1.f / l_run;  // rows past S (l = 0) are staged but never stored
 #pragma unroll
   for (int db = 0; db < NDB; ++db)
 #pragma unroll
@@ -369,8 +376,20 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_kernel(const AttnParams p) {
       uint2 w;
       w.x = pack_bf16x2(o[db][4 * g + 0] * inv_l, o[db][4 * g + 1] * inv_l);
       w.y = pack_bf16x2(o[db][4 * g + 2] * inv_l, o[db][4 * g + 3] * inv_l);
-      *reinterpret_cast<uint2*>(orow + db * 32 + 8 * g + 4 * hi) = w;
+      const int ch = (db * 4 + g) ^ (r32 % OCH);
+      *reinterpret_cast<uint2*>(ost + r32 * OROWB + ch * 16 + hi * 8) = w;
     }
+  // The wave's own LDS writes complete before its reads (and stay ahead of them).
+  __builtin_amdgcn_s_waitcnt(waitcnt_imm(63, 0));
+  const int jc = lane % OCH;
+  uint16_t* obase = p.out + (int64_t)h * HD + jc * 8;
+#pragma unroll
+  for (int i = 0; i < 32 / ORPI; ++i) {
+    const int r = i * ORPI + lane / OCH;
+    const uint4 v = *reinterpret_cast<const uint4*>(ost + r * OROWB + ((jc ^ (r % OCH)) << 4));
+    const int64_t mr = mw + r;
+    if (mr < S) *reinterpret_cast<uint4*>(obase + ((int64_t)b * S + mr) * ((int64_t)p.nq * HD)) = v;
+  }
 }
 
 template <int HD>
