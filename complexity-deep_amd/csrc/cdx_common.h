@@ -87,13 +87,7 @@ __device__ __forceinline__ uint4 pack8(const float* f) {
   return v;
 }
 
-// ---- wavefront helpers (wave64) -------------------------------------------
-__device__ __forceinline__ float wave_sum(float v) {
-#pragma unroll
-  for (int off = 32; off >= 1; off >>= 1) v += __shfl_xor(v, off, 64);
-  return v;
-}
-
+// ---- wavefront size --------------------------------------------------------
 constexpr int kWave = 64;
 
 }  // namespace cdx

@@ -180,12 +180,6 @@ __device__ __forceinline__ void buf_dma16(__amdgpu_buffer_rsrc_t r, uint32_t vof
                                            0, 0);
 }
 
-// 16 bytes from global memory straight into LDS at lds_block + 16 * lane.
-__device__ __forceinline__ void dma16(const uint16_t* g, uint8_t* lds_block) {
-  __builtin_amdgcn_global_load_lds((const __attribute__((address_space(1))) void*)g,
-                                   (__attribute__((address_space(3))) void*)lds_block, 16, 0, 0);
-}
-
 template <class Cfg, ALoad AL, Epi EP, int HD = 0>
 __global__ __launch_bounds__(kGemmThreads, Cfg::MINB) void gemm_nt_kernel(const GemmParams p) {
   constexpr int kBN = Cfg::BN, kBK = Cfg::BK, kStages = Cfg::STAGES;
