@@ -102,7 +102,8 @@ def test_moe_ragged(cdx, oracle, T, H, I, E, shared, V):
 @pytest.mark.parametrize("T,H,I,E,shared,empty", [(777, 16384, 704, 4, True, (1,)),
                                                   (1024, 16384, 1408, 8, False, (2, 3, 7)),
                                                   (4096, 8192, 4096, 64, True, (5, 6, 40)),
-                                                  (3000, 16384, 2048, 64, False, tuple(range(10, 50)))])
+                                                  (3000, 16384, 2048, 64, False, tuple(range(10, 50))),
+                                                  (200, 16384, 4096, 64, True, ()), (1, 16384, 704, 8, True, ())])
 def test_moe_down_tiles_across_experts(cdx, oracle, T, H, I, E, shared, empty):
     """Shapes whose down pass takes the M tiles that ignore expert boundaries: 16384
     output columns are 64 column tiles, so the up-to-one partial tile per expert would
@@ -110,7 +111,8 @@ def test_moe_down_tiles_across_experts(cdx, oracle, T, H, I, E, shared, empty):
     6 + 3; T=1024, no shared expert: 3 x 3 against 3 + 3).  Experts without tokens sit
     inside tiles that span experts, and the last tile is partial.  With 64 experts
     (the limit) of a few dozen tokens each, one tile spans many experts, and in the
-    last case a run of 40 empty experts sits inside one tile."""
+    fourth case a run of 40 empty experts sits inside one tile; with fewer than 256 tokens
+    one partial tile holds every expert (and a single token one row)."""
     print(f"moe spanning tiles T={T} H={H} E={E} shared={shared} empty={empty}", flush=True)
     g = torch.Generator().manual_seed(T)
     live = torch.tensor([e for e in range(E) if e not in empty])
