@@ -6,10 +6,13 @@ Interfaces follow the reference:
   fused_mu_qkv_projection    cuda/triton_mu_qkv.py:195-283 (weights [in, out])
   FusedMuQKVProjection       cuda/triton_mu_qkv.py:336-394
 
-The projection is one MFMA contraction over K = 2H: [x | mu_prev] @ W_pack^T with
-W_pack = [[Wq; Wk; Wv] | [Wmu_q; Wmu_k; Wmu_v]] packed once (cached per parameter
-version) instead of being concatenated on every forward (attention.py:122-124).  q,
-k and v are column slices of the packed [T, Nq*D + 2*Nkv*D] output.
+The projection is one MFMA contraction over K = 2H: [x | mu_prev] @ [W_x | W_mu]^T
+with W_x = [Wq; Wk; Wv] and W_mu = [Wmu_q; Wmu_k; Wmu_v], the kernel switching weight
+source at K = H.  The module keeps W_x and W_mu as two [N, H] buffers and its six
+Linear weights are row views of them, so nothing is concatenated per forward
+(attention.py:122-124 concatenates every call) and every write to a weight, through
+``.data`` or otherwise, reaches the kernel operand.  q, k and v are column slices of
+the packed [T, Nq*D + 2*Nkv*D] output.
 
 ComplexityAttention.forward goes one step further for head dims 32/64/128: the
 per-head QK RMSNorm and RoPE (attention.py:138-155) run in the projection kernel's
@@ -48,12 +51,37 @@ def _rows_view(t: torch.Tensor, H: int) -> Tuple[torch.Tensor, int]:
     return rows, ld
 
 
-def mu_qkv_project(x: torch.Tensor, mu: Optional[torch.Tensor], w_pack: torch.Tensor,
-                   H: int) -> torch.Tensor:
-    """[..., N] = [x | mu] @ w_pack^T (cdx_mu_qkv_fwd).
+def _weight_sources(w: torch.Tensor, w_mu: Optional[torch.Tensor], mu: Optional[torch.Tensor], H: int,
+                    what: str) -> Tuple[int, Optional[int], int]:
+    """(x-weight pointer, mu-weight pointer, common row stride) for the kernels.
 
-    w_pack is [N, 2H] (or [N, >=H] row-strided when mu is None)."""
-    nat.require_device(x, mu, w_pack, what="mu_qkv_project")
+    ``w`` is [N, >= H] (unit stride in K).  With ``w_mu`` None and a mu operand, ``w``
+    is a packed [N, >= 2H] whose columns [H, 2H) are the mu weights; otherwise
+    ``w_mu`` is [N, H] with the same row stride as ``w``."""
+    if w.dim() != 2 or w.stride(-1) != 1 or w.shape[1] < H:
+        raise ValueError(f"{what}: weight must be [N, >= {H}] with unit stride in K")
+    ldw = w.stride(0) if w.shape[0] > 1 else w.shape[1]
+    if mu is None:
+        return w.data_ptr(), None, ldw
+    if w_mu is None:
+        if w.shape[1] < 2 * H:
+            raise ValueError(f"{what}: a packed weight needs 2H = {2 * H} columns, got {w.shape[1]}")
+        return w.data_ptr(), w.data_ptr() + H * w.element_size(), ldw
+    if w_mu.dim() != 2 or w_mu.shape[0] != w.shape[0] or w_mu.shape[1] < H:
+        raise ValueError(f"{what}: mu weight shape {tuple(w_mu.shape)} does not match {tuple(w.shape)}")
+    ldm = w_mu.stride(0) if w_mu.shape[0] > 1 else ldw
+    if w_mu.stride(-1) != 1 or ldm != ldw or w_mu.dtype != w.dtype or w_mu.device != w.device:
+        raise ValueError(f"{what}: x and mu weights must share dtype, device and row stride")
+    return w.data_ptr(), w_mu.data_ptr(), ldw
+
+
+def mu_qkv_project(x: torch.Tensor, mu: Optional[torch.Tensor], w_pack: torch.Tensor,
+                   H: int, w_mu: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """[..., N] = [x | mu] @ [w_x | w_mu]^T (cdx_mu_qkv_fwd).
+
+    w_pack is [N, 2H] (x weights then mu weights) or, with ``w_mu`` given, the x
+    weights [N, H] alone; with mu=None only its first H columns are read."""
+    nat.require_device(x, mu, w_pack, w_mu, what="mu_qkv_project")
     lead = x.shape[:-1]
     x2, ldx = _rows_view(x, H)
     if ldx == 0:
@@ -67,13 +95,11 @@ def mu_qkv_project(x: torch.Tensor, mu: Optional[torch.Tensor], w_pack: torch.Te
         mu2, ldmu = _rows_view(mu, H)
     else:
         mu2, ldmu = None, 0
-    if w_pack.stride(-1) != 1:
-        raise ValueError("mu_qkv_project: packed weight must be unit-stride in K")
+    wx_ptr, wmu_ptr, ldw = _weight_sources(w_pack, w_mu, mu2, H, "mu_qkv_project")
     out = torch.empty(*lead, N, dtype=x.dtype, device=x.device)
     with nat.launch_region("mu_qkv", x.device, M=M, H=H, N=N, mu=mu2 is not None):
-        nat.check(nat.lib().cdx_mu_qkv_fwd(x2.data_ptr(), ldx, nat.ptr(mu2), ldmu, w_pack.data_ptr(),
-                                           w_pack.stride(0), M, H, N, out.data_ptr(), N,
-                                           nat.stream_of(x)), "cdx_mu_qkv_fwd")
+        nat.check(nat.lib().cdx_mu_qkv_fwd(x2.data_ptr(), ldx, nat.ptr(mu2), ldmu, wx_ptr, wmu_ptr, ldw,
+                                           M, H, N, out.data_ptr(), N, nat.stream_of(x)), "cdx_mu_qkv_fwd")
     return out
 
 
@@ -104,14 +130,15 @@ def to_vt_layout(v: torch.Tensor) -> torch.Tensor:
 
 def mu_qkv_rope(x: torch.Tensor, mu: Optional[torch.Tensor], w_pack: torch.Tensor, H: int, nq: int,
                 nkv: int, hd: int, q_norm_w: Optional[torch.Tensor], k_norm_w: Optional[torch.Tensor],
-                eps: float, cos_sin: torch.Tensor, pos0: int = 0, v_transposed: bool = False
-                ) -> Tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
+                eps: float, cos_sin: torch.Tensor, pos0: int = 0, v_transposed: bool = False,
+                w_mu: Optional[torch.Tensor] = None) -> Tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
     """(q, k, v) head-major [B, heads, S, hd] from x [B, S, H] (cdx_mu_qkv_rope_fwd):
     the mu-QKV projection with per-head RMSNorm of q and k (weights q_norm_w /
     k_norm_w, None = no norm) and RoPE at positions pos0 .. pos0+S-1 fused into one
-    kernel.  cos_sin is the fp32 [n_pos, hd/2, 2] table of RotaryEmbedding.
-    v_transposed=True returns V in the layout of to_vt_layout instead."""
-    nat.require_device(x, mu, w_pack, q_norm_w, k_norm_w, what="mu_qkv_rope")
+    kernel.  cos_sin is the fp32 [n_pos, hd/2, 2] table of RotaryEmbedding.  Weights
+    as in mu_qkv_project.  v_transposed=True returns V in the layout of to_vt_layout
+    instead."""
+    nat.require_device(x, mu, w_pack, w_mu, q_norm_w, k_norm_w, what="mu_qkv_rope")
     B, S, _ = x.shape
     x2, ldx = _rows_view(x, H)
     if ldx == 0:
@@ -121,8 +148,7 @@ def mu_qkv_rope(x: torch.Tensor, mu: Optional[torch.Tensor], w_pack: torch.Tenso
         mu2, ldmu = _rows_view(mu, H)
     else:
         mu2, ldmu = None, 0
-    if w_pack.stride(-1) != 1:
-        raise ValueError("mu_qkv_rope: packed weight must be unit-stride in K")
+    wx_ptr, wmu_ptr, ldw = _weight_sources(w_pack, w_mu, mu2, H, "mu_qkv_rope")
     if cos_sin.dtype != torch.float32 or not cos_sin.is_contiguous() or cos_sin.device != x.device:
         raise ValueError("mu_qkv_rope: cos_sin must be a contiguous fp32 table on the input's device")
     if (q_norm_w is None) != (k_norm_w is None):
@@ -145,7 +171,7 @@ def mu_qkv_rope(x: torch.Tensor, mu: Optional[torch.Tensor], w_pack: torch.Tenso
         v = torch.empty(B, nkv, S, hd, dtype=x.dtype, device=x.device)
     with nat.launch_region("mu_qkv", x.device, M=B * S, H=H, N=(nq + 2 * nkv) * hd, mu=mu2 is not None):
         nat.check(nat.lib().cdx_mu_qkv_rope_fwd(
-            x2.data_ptr(), ldx, nat.ptr(mu2), ldmu, w_pack.data_ptr(), w_pack.stride(0), B, S, H, nq, nkv, hd,
+            x2.data_ptr(), ldx, nat.ptr(mu2), ldmu, wx_ptr, wmu_ptr, ldw, B, S, H, nq, nkv, hd,
             nat.ptr(q_norm_w), nat.ptr(k_norm_w), float(eps), cos_sin.data_ptr(), cos_sin.shape[0], pos0,
             q.data_ptr(), k.data_ptr(), v.data_ptr(), vt_ld, nat.stream_of(x)), "cdx_mu_qkv_rope_fwd")
     return q, k, v
@@ -212,32 +238,62 @@ class FusedMuQKVProjection(nn.Module):
         self.mu_to_q = nn.Linear(hidden_size, self.q_dim, bias=False)
         self.mu_to_k = nn.Linear(hidden_size, self.kv_dim, bias=False)
         self.mu_to_v = nn.Linear(hidden_size, self.kv_dim, bias=False)
-        self._cache = _PackCache()
+        self._qkv_w = QKVWeights()
 
     def forward(self, x: torch.Tensor, mu: Optional[torch.Tensor] = None):
         forward_only("FusedMuQKVProjection", x, mu, *self.parameters())
-        w = self._cache.get(self)
-        out = mu_qkv_project(x, mu, w if mu is not None else w[:, : self.hidden_size], self.hidden_size)
+        w_x, w_mu = self._qkv_w.get(self)
+        out = mu_qkv_project(x, mu, w_x, self.hidden_size, w_mu=w_mu)
         return (out[..., : self.q_dim], out[..., self.q_dim: self.q_dim + self.kv_dim],
                 out[..., self.q_dim + self.kv_dim:])
 
 
-class _PackCache:
-    """W_pack = [[Wq; Wk; Wv] | [Wmu_q; Wmu_k; Wmu_v]] ([N, 2H]), rebuilt when a weight changes."""
+class QKVWeights:
+    """The kernel operands W_x = [Wq; Wk; Wv] and W_mu = [Wmu_q; Wmu_k; Wmu_v] of one
+    module, as one [2, N, H] buffer whose rows the six Linear weights are views of.
+
+    A write to a weight (in place, through ``.data``, by load_state_dict) therefore
+    lands in the operand the kernel reads; nothing is cached that could go stale.
+    When a weight is no longer its view (the module was moved or cast, a Parameter was
+    replaced), ``get`` copies the current weights into a new buffer and re-points them
+    at it.  The buffer is made outside inference mode, so that the weights stay
+    writable after a forward run under torch.inference_mode()."""
 
     def __init__(self):
-        self.key = None
-        self.w = None
+        self.buf: Optional[torch.Tensor] = None
+        self.ptrs = None
 
-    def get(self, m) -> torch.Tensor:
-        ws = (m.q_proj.weight, m.k_proj.weight, m.v_proj.weight,
-              m.mu_to_q.weight, m.mu_to_k.weight, m.mu_to_v.weight)
-        key = tuple((w.data_ptr(), w._version, w.dtype, w.device) for w in ws)
-        if key != self.key:
-            with torch.no_grad():
-                self.w = torch.cat([torch.cat(ws[:3], 0), torch.cat(ws[3:], 0)], 1).contiguous()
-            self.key = key
-        return self.w
+    @staticmethod
+    def _linears(m):
+        return (m.q_proj, m.k_proj, m.v_proj, m.mu_to_q, m.mu_to_k, m.mu_to_v)
+
+    def get(self, m) -> Tuple[torch.Tensor, torch.Tensor]:
+        ws = [lin.weight for lin in self._linears(m)]
+        if self.buf is None or [w.data_ptr() for w in ws] != self.ptrs:
+            self._bind(ws, m.hidden_size)
+        return self.buf[0], self.buf[1]
+
+    def _bind(self, ws, H: int) -> None:
+        dt, dev = ws[0].dtype, ws[0].device
+        if any(w.dtype != dt or w.device != dev or w.dim() != 2 or w.shape[1] != H for w in ws):
+            raise ValueError("ComplexityAttention: the q/k/v and mu_to_q/k/v weights must share one dtype "
+                             f"and device and be [out, {H}]")
+        xs, mus = ws[:3], ws[3:]
+        if [w.shape[0] for w in xs] != [w.shape[0] for w in mus]:
+            raise ValueError("ComplexityAttention: mu_to_q/k/v must have the shapes of q/k/v_proj")
+        N = sum(w.shape[0] for w in xs)
+        with torch.inference_mode(False), torch.no_grad():
+            buf = torch.empty(2, N, H, dtype=dt, device=dev)
+            r = 0
+            for wx, wm in zip(xs, mus):
+                n = wx.shape[0]
+                buf[0, r:r + n].copy_(wx)
+                buf[1, r:r + n].copy_(wm)
+                wx.data = buf[0, r:r + n]
+                wm.data = buf[1, r:r + n]
+                r += n
+        self.buf = buf
+        self.ptrs = [w.data_ptr() for w in ws]
 
 
 class ComplexityAttention(nn.Module):
@@ -272,14 +328,17 @@ class ComplexityAttention(nn.Module):
             self.k_norm = nn.RMSNorm(self.head_dim, eps=1e-6)
         self.rotary_emb = RotaryEmbedding(self.head_dim, max_seq_len=max_position_embeddings, theta=rope_theta)
         self.attention_dropout = attention_dropout
-        self._cache = _PackCache()
+        self._qkv_w = QKVWeights()
+
+    def qkv_weights(self) -> Tuple[torch.Tensor, torch.Tensor]:
+        """(W_x, W_mu), each [Nq*D + 2*Nkv*D, H]: the buffers the six projection weights
+        are views of, i.e. exactly what the kernels read."""
+        return self._qkv_w.get(self)
 
     def project_qkv(self, hidden_states: torch.Tensor, mu_prev: Optional[torch.Tensor]) -> torch.Tensor:
         """Packed [.., Nq*D + 2*Nkv*D] projection through the gfx950 MFMA kernel."""
-        w = self._cache.get(self)
-        if mu_prev is None:
-            w = w[:, : self.hidden_size]
-        return mu_qkv_project(hidden_states, mu_prev, w, self.hidden_size)
+        w_x, w_mu = self.qkv_weights()
+        return mu_qkv_project(hidden_states, mu_prev, w_x, self.hidden_size, w_mu=w_mu)
 
     @property
     def fused_prologue(self) -> bool:
@@ -311,25 +370,22 @@ class ComplexityAttention(nn.Module):
                 and not (self.training and self.attention_dropout > 0):
             # Whole attention on the kernels: fused projection (V written transposed) and
             # the causal GQA kernel, whose output is already merged over heads.
-            w = self._cache.get(self)
-            if mu_prev is None:
-                w = w[:, : self.hidden_size]
+            w_x, w_mu = self.qkv_weights()
             table = self.rotary_emb.cos_sin_table(S, hidden_states.device)
             qn = (self.q_norm.weight, self.k_norm.weight) if self.use_qk_norm else (None, None)
             eps = self.q_norm.eps if self.use_qk_norm else 0.0
-            q, k, vt = mu_qkv_rope(hidden_states, mu_prev, w, self.hidden_size, self.num_heads,
-                                   self.num_kv_heads, D, qn[0], qn[1], eps, table, 0, v_transposed=True)
+            q, k, vt = mu_qkv_rope(hidden_states, mu_prev, w_x, self.hidden_size, self.num_heads,
+                                   self.num_kv_heads, D, qn[0], qn[1], eps, table, 0, v_transposed=True,
+                                   w_mu=w_mu)
             return self._out_proj(causal_attention(q, k, vt), residual), None
         if self.fused_prologue:
             # Projection, head split, QK RMSNorm and RoPE in one kernel (attention.py:120-155).
-            w = self._cache.get(self)
-            if mu_prev is None:
-                w = w[:, : self.hidden_size]
+            w_x, w_mu = self.qkv_weights()
             table = self.rotary_emb.cos_sin_table(past_len + S, hidden_states.device)
             qn = (self.q_norm.weight, self.k_norm.weight) if self.use_qk_norm else (None, None)
             eps = self.q_norm.eps if self.use_qk_norm else 0.0
-            q, k, v = mu_qkv_rope(hidden_states, mu_prev, w, self.hidden_size, self.num_heads,
-                                  self.num_kv_heads, D, qn[0], qn[1], eps, table, past_len)
+            q, k, v = mu_qkv_rope(hidden_states, mu_prev, w_x, self.hidden_size, self.num_heads,
+                                  self.num_kv_heads, D, qn[0], qn[1], eps, table, past_len, w_mu=w_mu)
         else:
             q_dim, kv_dim = self.num_heads * D, self.num_kv_heads * D
             qkv = self.project_qkv(hidden_states, mu_prev)
@@ -364,4 +420,4 @@ class ComplexityAttention(nn.Module):
 MuGuidedAttention = ComplexityAttention
 
 __all__ = ["ComplexityAttention", "MuGuidedAttention", "FusedMuQKVProjection", "fused_mu_qkv_projection",
-           "mu_qkv_project", "mu_qkv_rope", "causal_attention", "to_vt_layout", "vt_columns"]
+           "mu_qkv_project", "mu_qkv_rope", "causal_attention", "to_vt_layout", "vt_columns", "QKVWeights"]

@@ -117,10 +117,13 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_kernel(const AttnParams p) {
   // ---- DMA sources ---------------------------------------------------------------
   // K tile row r (key n0 + r): chunk c at position c ^ ((r / K_RPL) % K_CPR).
   // V^T tile row d (keys n0 .. n0 + 63, 128 bytes): chunk c at position c ^ ((d / 2) % 8).
-  // Buffer loads straight to LDS: each lane's byte offset inside the (batch, kv head)
-  // slice is fixed and the tile's key position travels in the scalar offset.  The K
-  // descriptor covers exactly S rows, so rows past the end read as zeros (and are
-  // masked); V^T columns up to vt_ld are in range and finite by contract.
+  // Buffer loads straight to LDS, one descriptor per (batch, kv head) slice.  The K
+  // descriptor covers exactly S rows and the tile's row offset is added to each lane's
+  // vector offset, which the buffer range check always covers, so rows past the end
+  // read as zeros (and are masked) without leaving the K allocation; whether the
+  // check also covers the instruction's scalar offset is not relied on.  V^T tiles
+  // move along a row by their key position (scalar offset): columns up to vt_ld are
+  // inside the slice and finite by contract.
   const __amdgpu_buffer_rsrc_t rs_k =
       make_rsrc(p.k + ((int64_t)b * p.nkv + kvh) * S * HD, (uint32_t)(S * HD * 2));
   const __amdgpu_buffer_rsrc_t rs_v = make_rsrc(p.vt + ((int64_t)b * p.nkv + kvh) * HD * p.vt_ld);
@@ -136,10 +139,10 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_kernel(const AttnParams p) {
     v_off[j] = (uint32_t)((int64_t)d * p.vt_ld + ((lane % 8) ^ ((d / 2) % 8)) * 8) * 2;
   }
   auto issue_k = [&](int t, int buf) __attribute__((always_inline)) {
-    const uint32_t n0 = (uint32_t)t * kAttnBN;
+    const uint32_t tile_off = (uint32_t)t * (kAttnBN * HD * 2);
 #pragma unroll
     for (int j = 0; j < KPW; ++j)
-      buf_dma16(rs_k, k_off[j], n0 * HD * 2, lds + buf * K_BYTES + (wave * KPW + j) * 1024);
+      buf_dma16(rs_k, k_off[j] + tile_off, 0u, lds + buf * K_BYTES + (wave * KPW + j) * 1024);
   };
   auto issue_v = [&](int t, int buf) __attribute__((always_inline)) {
     const uint32_t n0 = (uint32_t)t * kAttnBN;
@@ -419,8 +422,9 @@ extern "C" int cdx_attention_fwd(const uint16_t* q, const uint16_t* k, const uin
   if (B == 0 || S == 0) return CDX_OK;
   if ((S + kAttnBM - 1) / kAttnBM > INT32_MAX || B * nq > INT32_MAX)
     return fail(CDX_EUNSUPPORTED, "%s: problem too large", name);
-  // The kernel addresses one (batch, kv head) slice of K and of V^T with 32-bit offsets.
-  if (S * hd * 2 > (int64_t)UINT32_MAX || vt_ld * hd * 2 > (int64_t)UINT32_MAX)
+  // The kernel addresses one (batch, kv head) slice of K and of V^T with 32-bit offsets;
+  // a K tile's offsets reach up to 64 rows past the slice (those rows read as zeros).
+  if ((S + 64) * hd * 2 > (int64_t)UINT32_MAX || vt_ld * hd * 2 > (int64_t)UINT32_MAX)
     return fail(CDX_EUNSUPPORTED, "%s: a K or V^T head slice must fit 4 GB (S=%lld)", name, (long long)S);
   if (!q || !k || !vt || !out) return fail(CDX_EINVAL, "%s: null pointer", name);
   if (!aligned16(q) || !aligned16(k) || !aligned16(vt) || !aligned16(out))

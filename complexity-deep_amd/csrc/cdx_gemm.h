@@ -97,6 +97,7 @@ struct GemmParams {
   int64_t M;
   // B operand: expert e uses b + e * b_estride, rows n with stride ldb
   const uint16_t* b;
+  const uint16_t* b2;  // concat: B columns [k_split, K) come from b2 (rows n, stride ldb)
   int64_t ldb;
   int64_t b_estride;
   int32_t N;
@@ -211,13 +212,20 @@ __global__ __launch_bounds__(kGemmThreads, Cfg::MINB) void gemm_nt_kernel(const 
   const int wm = wave >> 1, wn = wave & 1;
 
   // ---- tile decode -------------------------------------------------------
+  // Segment offsets are read clamped to [0, M] and a segment that ends before it
+  // starts is empty, so that offsets that are not a valid plan (the C-ABI cannot check
+  // device data) give wrong rows but no access outside the operands.
+  auto seg_off = [&](int x) __attribute__((always_inline)) {
+    const int v = p.offsets[x];
+    return v < 0 ? 0 : (v > (int)p.M ? (int)p.M : v);
+  };
   // Grouped GEMMs launch an upper bound of M tiles; the real count follows from the
   // segment offsets, so that the surplus blocks neither take an XCD's share nor sit
   // in the middle of the logical order.
   int mt_real = p.mt_count;
   if (AL != ALoad::kSegmented && p.offsets != nullptr) {
     mt_real = 0;
-    for (int x = 0; x < p.E; ++x) mt_real += (p.offsets[x + 1] - p.offsets[x] + kBM - 1) / kBM;
+    for (int x = 0; x < p.E; ++x) mt_real += max(0, (seg_off(x + 1) - seg_off(x) + kBM - 1) / kBM);
     mt_real = min(mt_real, p.mt_count);
   }
   const int L = xcd_remap(blockIdx.x, mt_real * p.nt_count);
@@ -233,26 +241,29 @@ __global__ __launch_bounds__(kGemmThreads, Cfg::MINB) void gemm_nt_kernel(const 
   const int mt = __builtin_amdgcn_readfirstlane(first_m + in_group % gsz);
   const int nt = __builtin_amdgcn_readfirstlane(in_group / gsz);
 
-  int64_t m0, m_end;
+  // The tile computes rows [m0, m0 + kBM) and stores rows [m_lo, m_end).
+  int64_t m0, m_end, m_lo;
   int e = 0;
   int e_lo = 0, n_exp = 1;  // kSegmented: first expert of the tile, experts it touches
   if constexpr (AL == ALoad::kSegmented) {
+    // Rows outside [offsets[0], offsets[E]) belong to no expert and are not stored.
     m0 = (int64_t)mt * kBM;
-    m_end = min(p.M, m0 + kBM);
-    if (m0 >= m_end) return;
-    // Experts holding rows m0 and m_end - 1 (segments are consecutive and sorted).
+    m_lo = max(m0, (int64_t)seg_off(0));
+    m_end = min(min(p.M, m0 + kBM), (int64_t)seg_off(p.E));
+    if (m_lo >= m_end) return;
+    // Experts holding rows m_lo and m_end - 1 (segments are consecutive and sorted).
     int e_hi = 0;
     for (int x = 0; x < p.E; ++x) {
-      if (p.offsets[x] <= m0 && m0 < p.offsets[x + 1]) e_lo = x;
-      if (p.offsets[x] <= m_end - 1 && m_end - 1 < p.offsets[x + 1]) e_hi = x;
+      if (seg_off(x) <= m_lo && m_lo < seg_off(x + 1)) e_lo = x;
+      if (seg_off(x) <= m_end - 1 && m_end - 1 < seg_off(x + 1)) e_hi = x;
     }
-    n_exp = e_hi - e_lo + 1;
+    n_exp = max(1, e_hi - e_lo + 1);
   } else if (p.offsets != nullptr) {
     int before = 0;
     e = -1;
     for (int x = 0; x < p.E; ++x) {
-      const int s0 = p.offsets[x], s1 = p.offsets[x + 1];
-      const int ntile = (s1 - s0 + kBM - 1) / kBM;
+      const int s0 = seg_off(x), s1 = seg_off(x + 1);
+      const int ntile = max(0, (s1 - s0 + kBM - 1) / kBM);
       if (mt < before + ntile) {
         e = x;
         m0 = s0 + (int64_t)(mt - before) * kBM;
@@ -262,9 +273,11 @@ __global__ __launch_bounds__(kGemmThreads, Cfg::MINB) void gemm_nt_kernel(const 
       before += ntile;
     }
     if (e < 0) return;
+    m_lo = m0;
   } else {
     m0 = (int64_t)mt * kBM;
     m_end = p.M;
+    m_lo = m0;
     if (m0 >= m_end) return;
   }
   const int n0 = nt * kBN;
@@ -282,9 +295,10 @@ __global__ __launch_bounds__(kGemmThreads, Cfg::MINB) void gemm_nt_kernel(const 
   // instruction's scalar offset, so a DMA costs no vector instruction.  Dense and
   // concat A and B offsets are relative to the tile's first row (< 4 GB for any
   // practical leading dimension); gathered A offsets are relative to the matrix,
-  // which the host bounds to 4 GB.  The concat descriptor's base sits k_split
-  // columns before mu's first column, so that both halves of K take the same scalar
-  // offset (2 k0) and the choice between them is a select, not a branch.
+  // which the host bounds to 4 GB.  The concat descriptors' bases (mu for A, the mu
+  // weights for B) sit k_split columns before their first column, so that both halves
+  // of K take the same scalar offset (2 k0) and the choice between the two sources is
+  // a select, not a branch.
   const int dr = lane / CPR;
   const uint16_t* bexp = p.b + (int64_t)e * p.b_estride;
   const uintptr_t a_base = (uintptr_t)(AL == ALoad::kGather ? p.a : p.a + m0 * p.lda);
@@ -292,10 +306,16 @@ __global__ __launch_bounds__(kGemmThreads, Cfg::MINB) void gemm_nt_kernel(const 
       AL == ALoad::kConcat ? (uintptr_t)(p.a2 + m0 * p.lda2) - (uintptr_t)p.k_split * 2 : a_base;
   // kSegmented: the A descriptor covers the tile's rows only, so that a masked row's
   // offset (kMaskedOff) reads zeros; each row remembers its expert (-1 past m_end).
+  // kGather: it covers the M source rows, so that a permutation entry outside them
+  // reads zeros instead of leaving the operand (the host bounds M * lda to 4 GB).
   const __amdgpu_buffer_rsrc_t rs_a =
       AL == ALoad::kSegmented ? make_rsrc((const void*)a_base, (uint32_t)((m_end - m0) * p.lda * 2))
+      : AL == ALoad::kGather  ? make_rsrc((const void*)a_base, (uint32_t)(p.M * p.lda * 2))
                               : make_rsrc((const void*)a_base);
   const __amdgpu_buffer_rsrc_t rs_b = make_rsrc(bexp + (int64_t)n0 * p.ldb);
+  const uintptr_t b_base = (uintptr_t)(bexp + (int64_t)n0 * p.ldb);
+  const uintptr_t b2_base =
+      AL == ALoad::kConcat ? (uintptr_t)(p.b2 + (int64_t)n0 * p.ldb) - (uintptr_t)p.k_split * 2 : b_base;
   constexpr uint32_t kMaskedOff = 0x80000000u;
   uint32_t a_off[LD_A], a2_off[LD_A], b_off[LD_B];
   int a_exp[AL == ALoad::kSegmented ? LD_A : 1];
@@ -306,15 +326,16 @@ __global__ __launch_bounds__(kGemmThreads, Cfg::MINB) void gemm_nt_kernel(const 
     int64_t gm = m0 + r;
     if constexpr (AL == ALoad::kSegmented) {
       int ex = -1;
-      if (gm < m_end) {
+      if (gm >= m_lo && gm < m_end) {
         ex = e_lo;
-        for (int x = e_lo + 1; x < e_lo + n_exp; ++x) ex += p.offsets[x] <= gm ? 1 : 0;
+        for (int x = e_lo + 1; x < e_lo + n_exp; ++x) ex += seg_off(x) <= gm ? 1 : 0;
       }
       a_exp[j] = ex;
     }
     gm = gm < m_end ? gm : m_end - 1;  // rows past the segment are loaded but never stored
     if (AL == ALoad::kGather) {
-      a_off[j] = (uint32_t)(((int64_t)p.perm[gm] * p.lda + dchunk * 8) * 2);
+      const int64_t src = p.perm[gm];
+      a_off[j] = (src < 0 || src >= p.M) ? kMaskedOff : (uint32_t)((src * p.lda + dchunk * 8) * 2);
     } else {
       a_off[j] = (uint32_t)(((gm - m0) * p.lda + dchunk * 8) * 2);
     }
@@ -385,6 +406,9 @@ __global__ __launch_bounds__(kGemmThreads, Cfg::MINB) void gemm_nt_kernel(const 
     } else {
       if constexpr (AL == ALoad::kSegmented) {
         const __amdgpu_buffer_rsrc_t r = make_rsrc((const void*)seg_bptr);
+        buf_dma16(live ? r : rs_none, b_off[d - LD_A], (uint32_t)k0 * 2, dst + b_dma_off + (d - LD_A) * 1024);
+      } else if constexpr (AL == ALoad::kConcat) {
+        const __amdgpu_buffer_rsrc_t r = make_rsrc((const void*)(k0 >= p.k_split ? b2_base : b_base));
         buf_dma16(live ? r : rs_none, b_off[d - LD_A], (uint32_t)k0 * 2, dst + b_dma_off + (d - LD_A) * 1024);
       } else {
         buf_dma16(live ? rs_b : rs_none, b_off[d - LD_A], (uint32_t)k0 * 2, dst + b_dma_off + (d - LD_A) * 1024);
@@ -776,7 +800,9 @@ __global__ __launch_bounds__(kGemmThreads, Cfg::MINB) void gemm_nt_kernel(const 
 #pragma unroll
     for (int i = 0; i < NIT; ++i) {
       const int64_t gm = m0 + wm * WM + i * RPI + lane / OUT_CH;
-      prow[i] = p.perm[gm < m_end ? gm : m_end - 1];
+      // Clamped into [0, M): a corrupt permutation scrambles rows but stays in C.
+      const int32_t pr = p.perm[gm < m_end ? gm : m_end - 1];
+      prow[i] = pr < 0 ? 0 : (pr >= (int32_t)p.M ? (int32_t)p.M - 1 : pr);
     }
   }
   if constexpr (EP == Epi::kScatterAdd) {
@@ -807,7 +833,7 @@ __global__ __launch_bounds__(kGemmThreads, Cfg::MINB) void gemm_nt_kernel(const 
   auto store_row = [&](int i) __attribute__((always_inline)) {
     const int r = i * RPI + lane / OUT_CH;
     const int64_t gm = m0 + wm * WM + r;
-    if (gm >= m_end) return;
+    if (gm < m_lo || gm >= m_end) return;
     const uint4 v = *reinterpret_cast<const uint4*>(ep + r * OUT_ROWB + ((jc ^ (r % OUT_CH)) << 4));
     const int col = jc * 8;  // first output column of the chunk within the wave
     uint16_t* dst;

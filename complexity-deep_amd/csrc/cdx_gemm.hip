@@ -1,5 +1,6 @@
 // C-ABI entry points built on the MFMA tile engine (cdx_gemm.h):
-//   cdx_mu_qkv_fwd       piece 2: one K = 2H contraction over [x | mu_prev]
+//   cdx_mu_qkv_fwd       piece 2: one K = 2H contraction over [x | mu_prev] against
+//                        [W_x | W_mu] (two weight sources, selected by the K half)
 //   cdx_mu_qkv_rope_fwd  the same contraction with QK RMSNorm + RoPE fused into the
 //                        epilogue, writing head-major q, k, v
 //   cdx_moe_swiglu_fwd   piece 1b: gather + gate/up + SwiGLU, then down + scatter,
@@ -38,8 +39,8 @@ using cdx::Epi;
 using cdx::GemmParams;
 
 extern "C" int cdx_mu_qkv_fwd(const uint16_t* x, int64_t ldx, const uint16_t* mu, int64_t ldmu,
-                              const uint16_t* w, int64_t ldw, int64_t M, int32_t H, int32_t N,
-                              uint16_t* out, int64_t ldo, void* stream) {
+                              const uint16_t* w, const uint16_t* w_mu, int64_t ldw, int64_t M, int32_t H,
+                              int32_t N, uint16_t* out, int64_t ldo, void* stream) {
   using namespace cdx;
   clear_error();
   const char* name = "cdx_mu_qkv_fwd";
@@ -47,13 +48,13 @@ extern "C" int cdx_mu_qkv_fwd(const uint16_t* x, int64_t ldx, const uint16_t* mu
   if (H % 64 != 0) return fail(CDX_EUNSUPPORTED, "%s: H=%d must be a multiple of 64", name, H);
   if (N % 8 != 0) return fail(CDX_EUNSUPPORTED, "%s: N=%d must be a multiple of 8", name, N);
   const int64_t K = mu ? 2 * (int64_t)H : (int64_t)H;
-  if (ldx < H || ldo < N || ldw < K || (mu && ldmu != 0 && ldmu < H))
+  if (ldx < H || ldo < N || ldw < H || (mu && ldmu != 0 && ldmu < H))
     return fail(CDX_EINVAL, "%s: leading dimension too small", name);
   if (ldx % 8 || ldo % 8 || ldw % 8 || (mu && ldmu % 8))
     return fail(CDX_EUNSUPPORTED, "%s: leading dimensions must be multiples of 8", name);
   if (M == 0) return CDX_OK;
-  if (!x || !w || !out) return fail(CDX_EINVAL, "%s: null pointer", name);
-  if (!aligned16(x) || !aligned16(w) || !aligned16(out) || (mu && !aligned16(mu)))
+  if (!x || !w || !out || (mu && !w_mu)) return fail(CDX_EINVAL, "%s: null pointer", name);
+  if (!aligned16(x) || !aligned16(w) || !aligned16(out) || (mu && (!aligned16(mu) || !aligned16(w_mu))))
     return fail(CDX_EUNSUPPORTED, "%s: pointers must be 16-byte aligned", name);
   GemmParams p{};
   p.a = x;
@@ -66,6 +67,7 @@ extern "C" int cdx_mu_qkv_fwd(const uint16_t* x, int64_t ldx, const uint16_t* mu
   p.E = 1;
   p.M = M;
   p.b = w;
+  p.b2 = w_mu;
   p.ldb = ldw;
   p.b_estride = 0;
   p.N = N;
@@ -213,7 +215,8 @@ extern "C" int cdx_grouped_gemm_fwd(const uint16_t* a, int64_t T, int32_t K, int
 }
 
 extern "C" int cdx_mu_qkv_rope_fwd(const uint16_t* x, int64_t ldx, const uint16_t* mu, int64_t ldmu,
-                                   const uint16_t* w, int64_t ldw, int64_t B, int64_t S, int32_t H,
+                                   const uint16_t* w, const uint16_t* w_mu, int64_t ldw, int64_t B, int64_t S,
+                                   int32_t H,
                                    int32_t nq, int32_t nkv, int32_t hd, const uint16_t* q_norm_w,
                                    const uint16_t* k_norm_w, float eps, const float* cos_sin,
                                    int64_t n_pos, int64_t pos0, uint16_t* q_out, uint16_t* k_out,
@@ -235,7 +238,7 @@ extern "C" int cdx_mu_qkv_rope_fwd(const uint16_t* x, int64_t ldx, const uint16_
   const int64_t K = mu ? 2 * (int64_t)H : (int64_t)H;
   if (N > INT32_MAX) return fail(CDX_EUNSUPPORTED, "%s: too many heads", name);
   if (S > INT32_MAX - 256) return fail(CDX_EUNSUPPORTED, "%s: S=%lld too long", name, (long long)S);
-  if (ldx < H || ldw < K || (mu && ldmu != 0 && ldmu < H))
+  if (ldx < H || ldw < H || (mu && ldmu != 0 && ldmu < H))
     return fail(CDX_EINVAL, "%s: leading dimension too small", name);
   if (ldx % 8 || ldw % 8 || (mu && ldmu % 8))
     return fail(CDX_EUNSUPPORTED, "%s: leading dimensions must be multiples of 8", name);
@@ -245,9 +248,11 @@ extern "C" int cdx_mu_qkv_rope_fwd(const uint16_t* x, int64_t ldx, const uint16_
   if (pos0 + S > n_pos)
     return fail(CDX_EINVAL, "%s: cos/sin table has %lld positions, needs %lld", name, (long long)n_pos,
                 (long long)(pos0 + S));
-  if (!x || !w || !cos_sin || !q_out || !k_out || !v_out) return fail(CDX_EINVAL, "%s: null pointer", name);
+  if (!x || !w || !cos_sin || !q_out || !k_out || !v_out || (mu && !w_mu))
+    return fail(CDX_EINVAL, "%s: null pointer", name);
   if (!aligned16(x) || !aligned16(w) || !aligned16(cos_sin) || !aligned16(q_out) || !aligned16(k_out) ||
-      !aligned16(v_out) || (mu && !aligned16(mu)) || (q_norm_w && (!aligned16(q_norm_w) || !aligned16(k_norm_w))))
+      !aligned16(v_out) || (mu && (!aligned16(mu) || !aligned16(w_mu))) ||
+      (q_norm_w && (!aligned16(q_norm_w) || !aligned16(k_norm_w))))
     return fail(CDX_EUNSUPPORTED, "%s: pointers must be 16-byte aligned", name);
   GemmParams p{};
   p.a = x;
@@ -258,6 +263,7 @@ extern "C" int cdx_mu_qkv_rope_fwd(const uint16_t* x, int64_t ldx, const uint16_
   p.E = 1;
   p.M = M;
   p.b = w;
+  p.b2 = w_mu;
   p.ldb = ldw;
   p.N = (int32_t)N;
   p.K = (int32_t)K;

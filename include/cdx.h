@@ -70,7 +70,8 @@ int cdx_add_rmsnorm_fwd(const uint16_t* x_dev, const uint16_t* residual_dev,
 
 /* ---- piece 1a: routing plan ------------------------------------------------ */
 
-/* Bytes of workspace cdx_route_plan needs for T tokens and E experts. */
+/* Bytes of workspace cdx_route_plan needs for T tokens and E experts: one int32 per
+ * (token block, expert), with at most 256 blocks, so never more than 64 KB. */
 size_t cdx_route_workspace_bytes(int64_t T, int32_t E);
 
 /*
@@ -165,17 +166,32 @@ int cdx_grouped_gemm_fwd(const uint16_t* a_dev, int64_t T, int32_t K, int32_t N,
                          const int32_t* offsets_dev, const uint16_t* w_dev,
                          uint16_t* out_dev, void* stream);
 
+/*
+ * Elementwise SwiGLU, out[i] = silu(gate[i]) * up[i], silu(g) = g / (1 + exp(-g)) in
+ * fp32.  dtype: 0 bf16, 1 fp16, 2 fp32 (gate, up and out all of it).
+ *   round_silu = 1: silu(gate) rounded to dtype, then multiplied by up and rounded
+ *                   (the reference's fused_swiglu_triton, and F.silu(g) * u);
+ *   round_silu = 0: silu(gate) * up in fp32, rounded once (fused_swiglu_simple).
+ * Pointers 16-byte aligned; any n >= 0.
+ *
+ * Replaces: cuda/triton_token_routed.py:234-257 (fused_swiglu_triton) and
+ * cuda/persistent_cggr.py:450-476 (fused_swiglu_simple).
+ */
+int cdx_swiglu_fwd(const void* gate_dev, const void* up_dev, int64_t n, int32_t dtype, int32_t round_silu,
+                   void* out_dev, void* stream);
+
 /* ---- piece 2: mu-guided QKV projection ------------------------------------- */
 
 /*
- * out[M, N] = [x | mu] @ w_pack^T, one K = 2H contraction, fp32 accumulate.
+ * out[M, N] = [x | mu] @ [w_x | w_mu]^T, one K = 2H contraction, fp32 accumulate.
  *   x      [M, H]  leading dim ldx
  *   mu     [M, H]  leading dim ldmu; ldmu == 0 broadcasts one row (layer 0's
  *                  mu_init.expand); mu == NULL means no mu term (K = H)
- *   w_pack [N, 2H] rows = output features, cols [0,H) the x weights
- *                  (q_proj|k_proj|v_proj rows stacked) and [H,2H) the mu weights
- *                  (mu_to_q|mu_to_k|mu_to_v).  With mu == NULL, w_pack is [N, H]
- *                  with leading dim ldw (ldw >= H).
+ *   w_x    [N, H]  rows = output features: the q_proj, k_proj, v_proj weights
+ *                  stacked ([out, in], as nn.Linear stores them), leading dim ldw
+ *   w_mu   [N, H]  the mu_to_q, mu_to_k, mu_to_v weights stacked, leading dim ldw;
+ *                  ignored when mu == NULL.  The two may be separate buffers or the
+ *                  two halves of one [N, 2H] pack (w_mu = w_x + H, ldw = 2H).
  *   out    [M, N]  leading dim ldo; q = cols [0, Nq*D), k, v follow.
  * H % 64 == 0.
  *
@@ -183,8 +199,8 @@ int cdx_grouped_gemm_fwd(const uint16_t* a_dev, int64_t T, int32_t K, int32_t N,
  * cuda/triton_mu_qkv.py:195-283 (fused_mu_qkv_projection).
  */
 int cdx_mu_qkv_fwd(const uint16_t* x_dev, int64_t ldx, const uint16_t* mu_dev, int64_t ldmu,
-                   const uint16_t* w_pack_dev, int64_t ldw, int64_t M, int32_t H, int32_t N,
-                   uint16_t* out_dev, int64_t ldo, void* stream);
+                   const uint16_t* w_x_dev, const uint16_t* w_mu_dev, int64_t ldw, int64_t M, int32_t H,
+                   int32_t N, uint16_t* out_dev, int64_t ldo, void* stream);
 
 /*
  * mu-QKV projection with the attention prologue fused into its epilogue:
@@ -201,7 +217,7 @@ int cdx_mu_qkv_fwd(const uint16_t* x_dev, int64_t ldx, const uint16_t* mu_dev, i
  *            with (cos, sin)(t_c) = cos_sin[pos0 + s][c mod hd/2], fp32 pairs, a table of
  *            n_pos >= pos0 + S positions (pos0 = tokens already in the KV cache).
  * q_norm_w / k_norm_w ([hd] bf16) both NULL: no QK norm.  hd must be 32, 64 or 128
- * and H a multiple of 64.  mu / ldmu / w_pack / ldw as in cdx_mu_qkv_fwd.
+ * and H a multiple of 64.  mu / ldmu / w_x / w_mu / ldw as in cdx_mu_qkv_fwd.
  * vt_ld == 0: v_out is [B, nkv, S, hd].  vt_ld > 0 (a multiple of 64, >= S): v_out is
  * V transposed for cdx_attention_fwd, [B, nkv, hd, vt_ld], token s of a sequence at
  * column 16*(s/16) + 4*sigma((s/4)%4) + s%4 with sigma = (0 2 1 3); the columns of
@@ -211,7 +227,8 @@ int cdx_mu_qkv_fwd(const uint16_t* x_dev, int64_t ldx, const uint16_t* mu_dev, i
  * k_norm, rotary tables and apply_rotary_pos_emb), core/rotary.py:57-86.
  */
 int cdx_mu_qkv_rope_fwd(const uint16_t* x_dev, int64_t ldx, const uint16_t* mu_dev, int64_t ldmu,
-                        const uint16_t* w_pack_dev, int64_t ldw, int64_t B, int64_t S, int32_t H,
+                        const uint16_t* w_x_dev, const uint16_t* w_mu_dev, int64_t ldw, int64_t B, int64_t S,
+                        int32_t H,
                         int32_t nq, int32_t nkv, int32_t hd, const uint16_t* q_norm_w_dev,
                         const uint16_t* k_norm_w_dev, float eps, const float* cos_sin_dev,
                         int64_t n_pos, int64_t pos0, uint16_t* q_out_dev, uint16_t* k_out_dev,

@@ -213,8 +213,13 @@ def grouped_gemm(sorted_tokens, expert_weights, offsets):
     return out
 
 
+def rope_inv_freq(head_dim: int, theta: float = 10000.0) -> torch.Tensor:
+    """fp32 theta^(-2i/D); rotary.py:35-36, evaluated on the CPU as at construction."""
+    return 1.0 / (theta ** (torch.arange(0, head_dim, 2).float() / head_dim))
+
+
 def rope_tables(inv_freq, seq_len: int):
-    """cos/sin [S, D] with emb = cat(freqs, freqs); rotary.py:30-47."""
+    """cos/sin [S, D] with emb = cat(freqs, freqs); rotary.py:40-47."""
     t = torch.arange(seq_len, dtype=torch.float32)
     freqs = torch.outer(t, _f32(inv_freq))
     emb = torch.cat([freqs, freqs], dim=-1)
@@ -243,7 +248,11 @@ def attention(x, mu, sd: Dict[str, torch.Tensor], prefix: str, cfg: dict):
     if cfg.get("use_qk_norm", True):
         q = rms_norm(q, g("q_norm.weight"), 1e-6)
         k = rms_norm(k, g("k_norm.weight"), 1e-6)
-    cos, sin = rope_tables(g("rotary_emb.inv_freq"), S)
+    # The reference builds its cos/sin cache in the constructor (rotary.py:38,40-47),
+    # from the fp32 inv_freq, before any cast of the model: the tables are therefore
+    # computed from (head_dim, rope_theta), not from the state_dict's inv_freq (which a
+    # bf16 state_dict holds rounded).
+    cos, sin = rope_tables(rope_inv_freq(D, cfg.get("rope_theta", 10000.0)), S)
     q = q * cos + _rotate_half(q) * sin
     k = k * cos + _rotate_half(k) * sin
     o = causal_attention(q, k, v)

@@ -66,9 +66,13 @@ def test_norm_validation(lib):
 
 
 def test_route_validation(lib):
+    # One int32 per (block, expert); blocks of 1024 tokens, at most 256 blocks.
     assert lib.cdx_route_workspace_bytes(0, 4) == 0
-    assert lib.cdx_route_workspace_bytes(1024, 4) == 2 * 1 * 4 * 4
-    assert lib.cdx_route_workspace_bytes(1025, 8) == 2 * 2 * 8 * 4
+    assert lib.cdx_route_workspace_bytes(1024, 4) == 1 * 4 * 4
+    assert lib.cdx_route_workspace_bytes(1025, 8) == 2 * 8 * 4
+    assert lib.cdx_route_workspace_bytes(256 * 1024, 64) == 256 * 64 * 4
+    assert lib.cdx_route_workspace_bytes(256 * 1024 + 1, 64) == 129 * 64 * 4  # blocks of 2048 tokens
+    assert lib.cdx_route_workspace_bytes(2 ** 31 - 1, 64) == 256 * 64 * 4
     assert lib.cdx_route_plan(16, 10, 16, 5, 65, 16, 16, 16, 16, 16, 16, 1 << 20, None) == CDX_EUNSUPPORTED
     assert lib.cdx_route_plan(16, 10, 16, 0, 4, 16, 16, 16, 16, 16, 16, 1 << 20, None) == CDX_EINVAL
     assert lib.cdx_route_plan(16, 2048, 16, 5, 4, 16, 16, 16, 16, 16, 16, 8, None) == CDX_EWORKSPACE
@@ -79,10 +83,11 @@ def test_route_validation(lib):
 
 
 def test_gemm_validation(lib):
-    assert lib.cdx_mu_qkv_fwd(16, 96, 16, 96, 16, 192, 8, 96, 64, 16, 64, None) == CDX_EUNSUPPORTED  # H % 64
-    assert lib.cdx_mu_qkv_fwd(16, 64, 16, 64, 16, 128, 8, 64, 60, 16, 64, None) == CDX_EUNSUPPORTED  # N % 8
-    assert lib.cdx_mu_qkv_fwd(16, 32, 16, 64, 16, 128, 8, 64, 64, 16, 64, None) == CDX_EINVAL  # ldx < H
-    assert lib.cdx_mu_qkv_fwd(16, 64, 16, 64, 16, 64, 8, 64, 64, 16, 64, None) == CDX_EINVAL  # ldw < 2H with mu
+    assert lib.cdx_mu_qkv_fwd(16, 96, 16, 96, 16, 16, 192, 8, 96, 64, 16, 64, None) == CDX_EUNSUPPORTED  # H % 64
+    assert lib.cdx_mu_qkv_fwd(16, 64, 16, 64, 16, 16, 128, 8, 64, 60, 16, 64, None) == CDX_EUNSUPPORTED  # N % 8
+    assert lib.cdx_mu_qkv_fwd(16, 32, 16, 64, 16, 16, 128, 8, 64, 64, 16, 64, None) == CDX_EINVAL  # ldx < H
+    assert lib.cdx_mu_qkv_fwd(16, 64, 16, 64, 16, 16, 32, 8, 64, 64, 16, 64, None) == CDX_EINVAL  # ldw < H
+    assert lib.cdx_mu_qkv_fwd(16, 64, 16, 64, 16, None, 64, 8, 64, 64, 16, 64, None) == CDX_EINVAL  # mu w/o w_mu
     assert lib.cdx_moe_swiglu_fwd(16, 8, 96, 64, 4, 1, 16, 16, 16, 16, 16, 16, None) == CDX_EUNSUPPORTED
     assert lib.cdx_moe_swiglu_fwd(16, 8, 64, 64, 65, 1, 16, 16, 16, 16, 16, 16, None) == CDX_EINVAL
     assert lib.cdx_moe_swiglu_fwd(None, 0, 64, 64, 4, 1, None, None, None, None, None, None, None) == 0

@@ -91,3 +91,27 @@ def test_attention_projection_and_operator_api(cdx, oracle):
     rq, rk, rv = oracle.mu_qkv(x.float().cpu(), mu.float().cpu(), *ws)
     ref = torch.cat([rq, rk, rv], -1)
     assert_close_bf16(packed, ref, "attention projection")
+
+
+def test_mu_qkv_split_weight_buffers(cdx):
+    """x and mu weights in two separate [N, H] buffers (the layout ComplexityAttention
+    keeps, its Linear weights being views of them) give the same bits as the packed
+    [N, 2H] form, for cdx_mu_qkv_fwd and cdx_mu_qkv_rope_fwd."""
+    from complexity_deep.attention import mu_qkv_project, mu_qkv_rope
+    from complexity_deep.rotary import RotaryEmbedding
+    print("mu_qkv split weights", flush=True)
+    B, S, H, nq, nkv, D = 2, 300, 512, 4, 2, 128
+    g = torch.Generator().manual_seed(21)
+    x = torch.randn(B, S, H, generator=g).to(bf16).cuda()
+    mu = torch.randn(B, S, H, generator=g).clamp(-2, 2).to(bf16).cuda()
+    ws = _weights(H, nq * D, nkv * D, 22)
+    packed = _pack(ws, H).cuda()
+    w_x = torch.cat(ws[:3], 0).cuda()
+    w_mu = torch.cat(ws[3:], 0).cuda()
+    assert torch.equal(mu_qkv_project(x, mu, w_x, H, w_mu=w_mu), mu_qkv_project(x, mu, packed, H))
+    table = RotaryEmbedding(D).cos_sin_table(S, torch.device("cuda"))
+    qn = torch.ones(D, dtype=bf16, device="cuda")
+    a = mu_qkv_rope(x, mu, w_x, H, nq, nkv, D, qn, qn, 1e-6, table, 0, v_transposed=True, w_mu=w_mu)
+    b = mu_qkv_rope(x, mu, packed, H, nq, nkv, D, qn, qn, 1e-6, table, 0, v_transposed=True)
+    for u, v in zip(a, b):
+        assert torch.equal(u, v)
