@@ -6,7 +6,9 @@ ModelOutput, create_complexity_model, count_parameters, TransformerBlock,
 MuGuidance, ComplexityAttention (alias MuGuidedAttention), TokenRoutedMLP, SwiGLU,
 RMSNorm, RotaryEmbedding, apply_rotary_pos_emb; and the operator functions
 fused_residual_rmsnorm, fused_add_rmsnorm_inplace, fused_rmsnorm,
-sort_tokens_by_expert, cggr_grouped_gemm, fused_mu_qkv_projection.
+sort_tokens_by_expert, sort_tokens_by_expert_fast, cggr_grouped_gemm (also as
+grouped_gemm_pytorch and persistent_cggr_gemm), persistent_swiglu_cggr,
+fused_swiglu_triton, fused_swiglu_simple, fused_mu_qkv_projection.
 
 The hot path (routing, MoE grouped SwiGLU GEMM, mu-QKV GEMM, add+RMSNorm) runs only
 on the kernels in libcdx.so; the forward is inference-only (no backward).
@@ -21,7 +23,9 @@ from .normalization import (FusedResidualRMSNorm, RMSNorm, fused_add_rmsnorm_inp
                             fused_rmsnorm)
 from .rotary import RotaryEmbedding, apply_rotary_pos_emb
 from .token_routed_mlp import (RoutePlan, TokenRoutedMLP, cggr_grouped_gemm, cggr_grouped_gemm_triton,
-                               route_plan, sort_tokens_by_expert)
+                               fused_swiglu_simple, fused_swiglu_triton, grouped_gemm_pytorch,
+                               persistent_cggr_gemm, persistent_swiglu_cggr, route_plan, sort_tokens_by_expert,
+                               sort_tokens_by_expert_fast)
 
 __version__ = "1.0.0"
 
@@ -30,6 +34,8 @@ __all__ = [
     "SwiGLU", "TokenRoutedMLP", "TransformerBlock", "MuGuidance", "ComplexityConfig", "ComplexityModel",
     "CausalLMOutput", "ModelOutput", "create_complexity_model", "count_parameters", "SIZE_PRESETS",
     "fused_residual_rmsnorm", "fused_add_rmsnorm_inplace", "fused_rmsnorm", "FusedResidualRMSNorm",
-    "sort_tokens_by_expert", "cggr_grouped_gemm", "cggr_grouped_gemm_triton", "route_plan", "RoutePlan",
+    "sort_tokens_by_expert", "sort_tokens_by_expert_fast", "cggr_grouped_gemm", "cggr_grouped_gemm_triton",
+    "grouped_gemm_pytorch", "persistent_cggr_gemm", "persistent_swiglu_cggr", "fused_swiglu_triton",
+    "fused_swiglu_simple", "route_plan", "RoutePlan",
     "fused_mu_qkv_projection", "FusedMuQKVProjection",
 ]

@@ -18,10 +18,11 @@ from . import _native as nat
 
 
 def identity_plan(T: int, device) -> RoutePlan:
+    """One expert holding every token in order (built on the device: no host copy)."""
     ar = torch.arange(T, dtype=torch.int32, device=device)
     return RoutePlan(expert_id=torch.zeros(T, dtype=torch.int32, device=device), perm=ar, inv_perm=ar,
                      counts=torch.full((1,), T, dtype=torch.int32, device=device),
-                     offsets=torch.tensor([0, T], dtype=torch.int32, device=device), num_experts=1)
+                     offsets=torch.arange(2, dtype=torch.int32, device=device) * T, num_experts=1)
 
 
 class SwiGLU(nn.Module):
@@ -32,6 +33,12 @@ class SwiGLU(nn.Module):
         self.gate_proj = nn.Linear(hidden_size, intermediate_size, bias=False)
         self.up_proj = nn.Linear(hidden_size, intermediate_size, bias=False)
         self.down_proj = nn.Linear(intermediate_size, hidden_size, bias=False)
+        self._key = None
+        self._packed = None
+
+    def refresh_packed_weights(self) -> None:
+        """Repack at the next forward (needed after writes through ``.data``, which bump
+        no version counter)."""
         self._key = None
         self._packed = None
 

@@ -212,6 +212,16 @@ class ComplexityModel(nn.Module):
                 mlp.token_to_expert.copy_(tmap.to(mlp.token_to_expert.device))
         return tmap
 
+    def refresh_packed_weights(self) -> None:
+        """Repack the MLP weights of every layer at the next forward.  Needed only after
+        writes through ``.data`` to MLP weights (they bump no version counter); the
+        attention projections need nothing, their weights are views of the kernel's
+        operands."""
+        for layer in self.layers:
+            fn = getattr(layer.mlp, "refresh_packed_weights", None)
+            if fn is not None:
+                fn()
+
     def route_plans(self, input_ids: torch.Tensor) -> List[Optional[RoutePlan]]:
         groups = self._map_grouping()
         plans: Dict[int, RoutePlan] = {}

@@ -1,11 +1,16 @@
 """Token-ID-routed MoE with the shared lexical expert on the gfx950 kernels (piece 1).
 
 Interfaces follow the reference:
-  TokenRoutedMLP            core/token_routed_mlp.py:28-194 (same constructor,
-                            parameters, buffer and state_dict keys)
-  sort_tokens_by_expert     cuda/triton_token_routed.py:37-61
-  cggr_grouped_gemm         cuda/triton_token_routed.py:197-231 (and the PyTorch
-                            grouped_gemm_pytorch of :64-86)
+  TokenRoutedMLP              core/token_routed_mlp.py:28-194 (same constructor,
+                              parameters, buffer and state_dict keys)
+  sort_tokens_by_expert       cuda/triton_token_routed.py:37-61
+  sort_tokens_by_expert_fast  cuda/persistent_cggr.py:318-352
+  cggr_grouped_gemm           cuda/triton_token_routed.py:197-231 (also under the
+                              names grouped_gemm_pytorch, :64-86, and
+                              persistent_cggr_gemm, cuda/persistent_cggr.py:355-410)
+  persistent_swiglu_cggr      cuda/persistent_cggr.py:479-530
+  fused_swiglu_triton         cuda/triton_token_routed.py:234-257
+  fused_swiglu_simple         cuda/persistent_cggr.py:450-476
 
 The forward is: route plan (cdx_route_plan: expert lookup, counts, offsets, stable
 permutation) -> cdx_moe_swiglu_fwd (gathered gate/up GEMM with SwiGLU epilogue,
@@ -115,9 +120,34 @@ def sort_tokens_by_expert(tokens: torch.Tensor, expert_ids: torch.Tensor, num_ex
     return sorted_tokens, plan.perm.to(torch.int64), plan.offsets.to(torch.int64), plan.counts.to(torch.int64)
 
 
+def sort_tokens_by_expert_fast(token_ids: torch.Tensor, expert_mapping: torch.Tensor, num_experts: int
+                               ) -> Tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
+    """(sorted_indices, expert_offsets [E+1], expert_counts [E]), all int64, of the token
+    ids routed through ``expert_mapping`` (ids clamped to the vocabulary);
+    cuda/persistent_cggr.py:318-352.  One cdx_route_plan; the order inside an expert
+    is the original token order."""
+    plan = route_plan(token_ids, expert_mapping, num_experts)
+    return plan.perm.to(torch.int64), plan.offsets.to(torch.int64), plan.counts.to(torch.int64)
+
+
+def _offsets_i32(expert_offsets: torch.Tensor, E: int, device: torch.device) -> torch.Tensor:
+    offs = torch.as_tensor(expert_offsets)
+    if offs.dim() != 1 or offs.numel() != E + 1:
+        raise ValueError(f"expert_offsets must have num_experts + 1 = {E + 1} entries, got {tuple(offs.shape)}")
+    # Values are not inspected on the host (that would synchronise): the kernels read
+    # them clamped to [0, rows], and rows outside [offsets[0], offsets[E]) stay zero.
+    return offs.to(device=device, dtype=torch.int32).contiguous()
+
+
+def _aligned_rows(t: torch.Tensor) -> torch.Tensor:
+    """Contiguous with a 16-byte aligned base (the kernels' DMA needs both)."""
+    t = t.contiguous()
+    return t if t.data_ptr() % 16 == 0 else t.clone()
+
+
 def cggr_grouped_gemm(sorted_tokens: torch.Tensor, expert_weights: torch.Tensor,
                       expert_offsets: torch.Tensor) -> torch.Tensor:
-    """out[o_e:o_{e+1}] = sorted_tokens[o_e:o_{e+1}] @ expert_weights[e];
+    """out[o_e:o_{e+1}] = sorted_tokens[o_e:o_{e+1}] @ expert_weights[e], zero elsewhere;
     cuda/triton_token_routed.py:197-231.  expert_weights is [E, in, out] (bf16)."""
     forward_only("cggr_grouped_gemm", sorted_tokens, expert_weights)
     nat.require_device(sorted_tokens, expert_weights, what="cggr_grouped_gemm")
@@ -125,17 +155,65 @@ def cggr_grouped_gemm(sorted_tokens: torch.Tensor, expert_weights: torch.Tensor,
     E, K2, N = expert_weights.shape
     if K2 != K:
         raise ValueError(f"cggr_grouped_gemm: in_dim mismatch {K} vs {K2}")
-    a = sorted_tokens.contiguous()
+    a = _aligned_rows(sorted_tokens)
     w_t = expert_weights.transpose(1, 2).contiguous()  # [E, N, K], K-contiguous
-    offs = expert_offsets.to(device=a.device, dtype=torch.int32).contiguous()
-    out = torch.empty(T, N, dtype=a.dtype, device=a.device)
-    nat.check(nat.lib().cdx_grouped_gemm_fwd(a.data_ptr(), T, K, N, E, offs.data_ptr(), w_t.data_ptr(),
-                                             out.data_ptr(), nat.stream_of(a)), "cdx_grouped_gemm_fwd")
+    offs = _offsets_i32(expert_offsets, E, a.device)
+    out = torch.zeros(T, N, dtype=a.dtype, device=a.device)
+    with nat.launch_region("grouped_gemm", a.device, T=T, K=K, N=N, E=E):
+        nat.check(nat.lib().cdx_grouped_gemm_fwd(a.data_ptr(), T, K, N, E, offs.data_ptr(), w_t.data_ptr(),
+                                                 out.data_ptr(), nat.stream_of(a)), "cdx_grouped_gemm_fwd")
     return out
 
 
 cggr_grouped_gemm_triton = cggr_grouped_gemm
 grouped_gemm = cggr_grouped_gemm
+
+
+def grouped_gemm_pytorch(sorted_tokens: torch.Tensor, expert_weights: torch.Tensor, expert_offsets: torch.Tensor,
+                         expert_counts: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """cuda/triton_token_routed.py:64-86 (the counts argument is not needed: the segments
+    are expert_offsets).  Runs on cdx_grouped_gemm_fwd like cggr_grouped_gemm."""
+    return cggr_grouped_gemm(sorted_tokens, expert_weights, expert_offsets)
+
+
+def persistent_cggr_gemm(sorted_tokens: torch.Tensor, expert_weights: torch.Tensor, expert_offsets: torch.Tensor,
+                         num_sms: int = 80) -> torch.Tensor:
+    """cuda/persistent_cggr.py:355-410.  ``num_sms`` is accepted for API compatibility:
+    the grid here is sized by the kernel from the tile count and the chip's XCDs."""
+    return cggr_grouped_gemm(sorted_tokens, expert_weights, expert_offsets)
+
+
+_DTYPE_CODE = {torch.bfloat16: 0, torch.float16: 1, torch.float32: 2}
+
+
+def _swiglu(gate: torch.Tensor, up: torch.Tensor, round_silu: bool, what: str) -> torch.Tensor:
+    nat.require_device(gate, up, dtype=None, what=what)
+    if gate.shape != up.shape or gate.dtype != up.dtype:
+        raise ValueError(f"{what}: gate {tuple(gate.shape)} {gate.dtype} and up {tuple(up.shape)} {up.dtype} differ")
+    code = _DTYPE_CODE.get(gate.dtype)
+    if code is None:
+        raise ValueError(f"{what}: dtype {gate.dtype} not supported (bf16, fp16, fp32)")
+    g, u = _aligned_rows(gate), _aligned_rows(up)
+    out = torch.empty(gate.shape, dtype=gate.dtype, device=gate.device)
+    with nat.launch_region("swiglu", gate.device, n=g.numel(), elt=g.element_size()):
+        nat.check(nat.lib().cdx_swiglu_fwd(g.data_ptr(), u.data_ptr(), g.numel(), code, int(round_silu),
+                                           out.data_ptr(), nat.stream_of(g)), "cdx_swiglu_fwd")
+    return out
+
+
+def fused_swiglu_triton(gate: torch.Tensor, up: torch.Tensor) -> torch.Tensor:
+    """silu(gate) * up with silu rounded to the dtype first (cdx_swiglu_fwd, round_silu=1);
+    cuda/triton_token_routed.py:234-257.  Non-contiguous inputs (the halves of a fused
+    gate/up output) are made contiguous, as there."""
+    forward_only("fused_swiglu_triton", gate, up)
+    return _swiglu(gate, up, True, "fused_swiglu_triton")
+
+
+def fused_swiglu_simple(gate: torch.Tensor, up: torch.Tensor) -> torch.Tensor:
+    """silu(gate) * up in fp32, rounded once (cdx_swiglu_fwd, round_silu=0);
+    cuda/persistent_cggr.py:450-476."""
+    forward_only("fused_swiglu_simple", gate, up)
+    return _swiglu(gate, up, False, "fused_swiglu_simple")
 
 
 # ---------------------------------------------------------------------------
@@ -189,8 +267,13 @@ def moe_swiglu(x2d: torch.Tensor, plan: RoutePlan, w_gu: torch.Tensor, w_down: t
 
     With ``residual`` ([T, H], contiguous) the rows are added to it in place instead
     (cdx_moe_swiglu_residual_fwd) and ``residual`` is returned."""
+    return _moe_swiglu(x2d, plan.perm, plan.offsets, plan.num_experts, w_gu, w_down, ie, has_shared, residual)
+
+
+def _moe_swiglu(x2d: torch.Tensor, perm: torch.Tensor, offsets: torch.Tensor, E: int, w_gu: torch.Tensor,
+                w_down: torch.Tensor, ie: int, has_shared: bool, residual: Optional[torch.Tensor] = None
+                ) -> torch.Tensor:
     T, H = x2d.shape
-    E = plan.num_experts
     P = padded_width(ie)
     S = 2 if has_shared else 1
     if w_gu.shape != (E, 2 * S * P, H) or w_down.shape != (E, H, S * P):
@@ -204,10 +287,39 @@ def moe_swiglu(x2d: torch.Tensor, plan: RoutePlan, w_gu: torch.Tensor, w_down: t
         out, fn, fname = torch.empty_like(x2d), nat.lib().cdx_moe_swiglu_fwd, "cdx_moe_swiglu_fwd"
     inter = torch.empty(T, S * P, dtype=x2d.dtype, device=x2d.device)
     with nat.launch_region("moe_swiglu", x2d.device, T=T, H=H, Ie=ie, E=E, shared=has_shared):
-        nat.check(fn(x2d.data_ptr(), T, H, ie, E, int(has_shared), plan.perm.data_ptr(), plan.offsets.data_ptr(),
+        nat.check(fn(x2d.data_ptr(), T, H, ie, E, int(has_shared), perm.data_ptr(), offsets.data_ptr(),
                      w_gu.data_ptr(), w_down.data_ptr(), inter.data_ptr(), out.data_ptr(), nat.stream_of(x2d)),
                   fname)
     return out
+
+
+def persistent_swiglu_cggr(sorted_tokens: torch.Tensor, gate_weights: torch.Tensor, up_weights: torch.Tensor,
+                           down_weights: torch.Tensor, expert_offsets: torch.Tensor, num_sms: int = 80
+                           ) -> torch.Tensor:
+    """SwiGLU experts over tokens already sorted by expert; cuda/persistent_cggr.py:479-530.
+
+    out[o_e:o_{e+1}] = (silu(t @ gate[e]) * (t @ up[e])) @ down[e] for t the rows of
+    segment e, zero outside [offsets[0], offsets[E]).  gate/up [E, H, I] and down
+    [E, I, H] ([in, out], bf16).  Both GEMMs run on cdx_moe_swiglu_fwd with an
+    identity permutation and no shared block; the gate/up products stay fp32 into
+    the SwiGLU, which is rounded once (the reference rounds the two products to bf16
+    first).  The weights are packed on every call, as the operator holds no state.
+    ``num_sms`` is accepted for API compatibility."""
+    forward_only("persistent_swiglu_cggr", sorted_tokens, gate_weights, up_weights, down_weights)
+    nat.require_device(sorted_tokens, gate_weights, up_weights, down_weights, what="persistent_swiglu_cggr")
+    if sorted_tokens.dim() != 2:
+        raise ValueError("persistent_swiglu_cggr: sorted_tokens must be [tokens, hidden]")
+    T, H = sorted_tokens.shape
+    E, H2, ie = gate_weights.shape
+    if H2 != H or up_weights.shape != gate_weights.shape or down_weights.shape != (E, ie, H):
+        raise ValueError("persistent_swiglu_cggr: weight shapes must be gate/up [E, H, I] and down [E, I, H]")
+    x = _aligned_rows(sorted_tokens)
+    w_gu, w_down = pack_moe_weights(gate_weights, up_weights, down_weights, None, None, None)
+    offs = _offsets_i32(expert_offsets, E, x.device)
+    ident = torch.arange(T, dtype=torch.int32, device=x.device)
+    # Rows are added into zeros (one exact add): rows that no segment covers stay zero.
+    out = torch.zeros(T, H, dtype=x.dtype, device=x.device)
+    return _moe_swiglu(x, ident, offs, E, w_gu, w_down, ie, False, residual=out)
 
 
 # ---------------------------------------------------------------------------
@@ -260,6 +372,16 @@ class TokenRoutedMLP(nn.Module):
         nat.check(nat.lib().cdx_binpack_map(freq.data_ptr(), vocab_size, num_experts, mapping.data_ptr()),
                   "cdx_binpack_map")
         return mapping
+
+    def refresh_packed_weights(self) -> None:
+        """Drop the kernel-layout copies, so the next forward packs the parameters anew.
+
+        In-place writes to a parameter bump its version and are picked up without this;
+        writes through ``.data`` (``p.data.zero_()``) bump no version counter and need
+        this call."""
+        self._pack_key = None
+        self._packed = None
+        self._all_key = None
 
     def packed_weights(self) -> Tuple[torch.Tensor, torch.Tensor]:
         """Kernel-layout weights, rebuilt only when a parameter changes (never saved)."""
@@ -327,11 +449,7 @@ class TokenRoutedMLP(nn.Module):
             self._all_width = gate.shape[1]
             self._all_key = key
         T = x2d.shape[0]
-        plan = RoutePlan(expert_id=torch.zeros(T, dtype=torch.int32, device=x2d.device),
-                         perm=torch.arange(T, dtype=torch.int32, device=x2d.device),
-                         inv_perm=torch.arange(T, dtype=torch.int32, device=x2d.device),
-                         counts=torch.tensor([T], dtype=torch.int32, device=x2d.device),
-                         offsets=torch.tensor([0, T], dtype=torch.int32, device=x2d.device),
-                         num_experts=1)
+        ident = torch.arange(T, dtype=torch.int32, device=x2d.device)
+        offsets = torch.arange(2, dtype=torch.int32, device=x2d.device) * T
         w_gu, w_down = self._all_packed
-        return moe_swiglu(x2d, plan, w_gu, w_down, self._all_width, False)
+        return _moe_swiglu(x2d, ident, offsets, 1, w_gu, w_down, self._all_width, False)
