@@ -4,27 +4,42 @@
 // :166-170 (mask dispatch, i.e. a stable partition by expert id) and the operator
 // API cuda/triton_token_routed.py:37-61 (counts = bincount, offsets = [0, cumsum]).
 //
-// Design: a stable counting sort in three launches, bit-exact and free of atomics.
-//   1. count:   each 256-thread block owns 1024 consecutive tokens, split into 16
-//               chunks of 64 (one chunk per wave per step).  A wave looks up the
-//               expert of its 64 tokens and, per expert, takes a 64-bit ballot; the
-//               popcount is the chunk's count.  The block writes its per-expert
-//               totals to workspace row [block][E].
-//   2. scan:    one block turns the [nblk][E] counts into counts/offsets and into the
-//               first sorted position of every (block, expert) pair, scanning in
-//               expert-major, block-minor order.
-//   3. scatter: each block recomputes its ballots; a token's sorted position is
-//               base[block][e] + (tokens of e in earlier chunks of the block) +
-//               popcount(ballot & lanes-below).  Token order inside an expert is the
-//               original index order, which is exactly argsort(expert, stable=True).
+// Design: a stable counting sort in two launches, bit-exact and deterministic.
+// Tokens are split into at most kMaxBlocks blocks of tpb consecutive tokens (tpb a
+// multiple of 1024, the smallest that keeps the block count within kMaxBlocks); a
+// block walks its tokens in rounds of 1024 = 16 chunks of 64, one chunk per wave.
+//   1. count:   each block looks up the expert of its tokens (written to expert_id)
+//               and, per chunk and expert, takes a 64-bit ballot; the popcounts summed
+//               in LDS (integer adds: order-free) are the block's per-expert totals,
+//               written to row [block][E] of a small count table.
+//   2. scatter: every block reads the whole count table (at most kMaxBlocks x E ints)
+//               and derives, per expert, the total (hence counts and offsets; block 0
+//               writes them) and the tokens of earlier blocks (its base).  It then
+//               recomputes its ballots round by round: a token's sorted position is
+//               base[e] + (tokens of e in earlier chunks) + popcount(ballot & lanes
+//               below).  Token order inside an expert is the original index order,
+//               which is exactly argsort(expert, stable=True).
+// The count table is the only scratch: caller workspace (cdx_route_plan) or a
+// library-owned device array (cdx_route_plan_noalloc).  Nothing needs zeroing: the
+// count launch writes every entry the scatter launch reads.
+#include <mutex>
+
 #include "cdx_common.h"
 
 namespace cdx {
 namespace {
 
-constexpr int kTokPerBlock = 1024;
-constexpr int kChunks = kTokPerBlock / kWave;  // 16
+constexpr int kRound = 1024;                 // tokens per round of a block
+constexpr int kChunks = kRound / kWave;      // 16 chunks of 64
 constexpr int kMaxE = 64;
+constexpr int kMaxBlocks = 256;
+constexpr int kScratchInts = kMaxBlocks * kMaxE;  // 64 KB: the largest count table
+
+// Tokens per block: a multiple of kRound such that the block count is <= kMaxBlocks.
+inline int64_t tokens_per_block(int64_t T) {
+  const int64_t rounds = (T + (int64_t)kRound * kMaxBlocks - 1) / ((int64_t)kRound * kMaxBlocks);
+  return kRound * (rounds < 1 ? 1 : rounds);
+}
 
 __device__ __forceinline__ int lookup_expert(const int64_t* ids, const int64_t* map, int64_t V,
                                              int E, int64_t t) {
@@ -42,165 +57,198 @@ __device__ __forceinline__ int lookup_expert(const int64_t* ids, const int64_t* 
 }
 
 __global__ __launch_bounds__(256) void route_count_kernel(const int64_t* __restrict__ ids,
-                                                          const int64_t* __restrict__ map,
-                                                          int64_t V, int E, int64_t T,
+                                                          const int64_t* __restrict__ map, int64_t V, int E,
+                                                          int64_t T, int64_t tpb,
                                                           int32_t* __restrict__ expert_id,
                                                           int32_t* __restrict__ blk_counts) {
+  __shared__ int cnt[kMaxE];
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  if (threadIdx.x < E) cnt[threadIdx.x] = 0;
+  __syncthreads();
+  const int64_t b0 = (int64_t)blockIdx.x * tpb;
+  const int64_t b1 = min(T, b0 + tpb);
+  for (int64_t r0 = b0; r0 < b1; r0 += kRound) {
+    // The four chunks of a wave: lookups first (independent loads in flight), then
+    // the ballots.
+    int ev[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int64_t t = r0 + (wave * 4 + j) * kWave + lane;
+      ev[j] = t < b1 ? lookup_expert(ids, map, V, E, t) : -1;
+      if (t < b1) expert_id[t] = ev[j];
+    }
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+      for (int x = 0; x < E; ++x) {
+        const uint64_t m = __ballot(ev[j] == x);
+        if (lane == 0 && m) atomicAdd(&cnt[x], __popcll(m));
+      }
+  }
+  __syncthreads();
+  if (threadIdx.x < E) blk_counts[(int64_t)blockIdx.x * E + threadIdx.x] = cnt[threadIdx.x];
+}
+
+__global__ __launch_bounds__(256) void route_scatter_kernel(const int32_t* __restrict__ expert_id, int E,
+                                                            int64_t T, int64_t tpb, int nblk,
+                                                            const int32_t* __restrict__ blk_counts,
+                                                            int32_t* __restrict__ perm, int32_t* __restrict__ inv_perm,
+                                                            int32_t* __restrict__ counts,
+                                                            int32_t* __restrict__ offsets) {
   __shared__ int cnt[kChunks][kMaxE];
+  __shared__ int pre[kChunks][kMaxE];
+  __shared__ int total[kMaxE];
+  __shared__ int base[kMaxE];
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
-  const int64_t base = (int64_t)blockIdx.x * kTokPerBlock;
-#pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    const int c = wave * 4 + j;
-    const int64_t t = base + c * kWave + lane;
-    int e = -1;
-    if (t < T) {
-      e = lookup_expert(ids, map, V, E, t);
-      expert_id[t] = e;
-    }
-    for (int x = 0; x < E; ++x) {
-      const uint64_t m = __ballot(e == x);
-      if (lane == 0) cnt[c][x] = __popcll(m);
-    }
-  }
-  __syncthreads();
-  for (int x = threadIdx.x; x < E; x += blockDim.x) {
-    int s = 0;
-#pragma unroll
-    for (int c = 0; c < kChunks; ++c) s += cnt[c][x];
-    blk_counts[(int64_t)blockIdx.x * E + x] = s;
-  }
-}
+  const int blk = blockIdx.x;
 
-// Inclusive scan of one int per thread over a 1024-thread block.
-__device__ __forceinline__ int block_inclusive_scan(int v, int* lds_wave_tot, int& block_total) {
-  const int lane = threadIdx.x & 63;
-  const int wave = threadIdx.x >> 6;
-#pragma unroll
-  for (int off = 1; off < 64; off <<= 1) {
-    const int y = __shfl_up(v, off, 64);
-    if (lane >= off) v += y;
-  }
-  if (lane == 63) lds_wave_tot[wave] = v;
-  __syncthreads();
-  int prefix = 0, total = 0;
-  const int nw = blockDim.x >> 6;
-  for (int w = 0; w < nw; ++w) {
-    const int tw = lds_wave_tot[w];
-    if (w < wave) prefix += tw;
-    total += tw;
-  }
-  __syncthreads();
-  block_total = total;
-  return v + prefix;
-}
-
-__global__ __launch_bounds__(1024) void route_scan_kernel(int64_t nblk, int E,
-                                                          const int32_t* __restrict__ blk_counts,
-                                                          int32_t* __restrict__ blk_base,
-                                                          int32_t* __restrict__ counts,
-                                                          int32_t* __restrict__ offsets) {
-  __shared__ int wave_tot[16];
-  __shared__ int totals[kMaxE];
-  __shared__ int offs[kMaxE + 1];
-  for (int x = 0; x < E; ++x) {
-    int carry = 0;
-    for (int64_t b0 = 0; b0 < nblk; b0 += blockDim.x) {
-      const int64_t b = b0 + threadIdx.x;
-      const int v = b < nblk ? blk_counts[b * E + x] : 0;
-      int tot;
-      const int incl = block_inclusive_scan(v, wave_tot, tot);
-      if (b < nblk) blk_base[b * E + x] = carry + incl - v;  // exclusive, within expert x
-      carry += tot;
+  // Per expert: all blocks' tokens (total) and those of blocks before this one.
+  for (int x = wave; x < E; x += 4) {
+    int tot = 0, before = 0;
+    for (int b = lane; b < nblk; b += kWave) {
+      const int v = blk_counts[(int64_t)b * E + x];
+      tot += v;
+      before += b < blk ? v : 0;
     }
-    if (threadIdx.x == 0) totals[x] = carry;
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) {
+      tot += __shfl_xor(tot, off, 64);
+      before += __shfl_xor(before, off, 64);
+    }
+    if (lane == 0) {
+      total[x] = tot;
+      base[x] = before;
+    }
   }
   __syncthreads();
   if (threadIdx.x == 0) {
     int run = 0;
-    offs[0] = 0;
     for (int x = 0; x < E; ++x) {
-      run += totals[x];
-      offs[x + 1] = run;
+      if (blk == 0) {
+        counts[x] = total[x];
+        offsets[x] = run;
+      }
+      base[x] += run;
+      run += total[x];
     }
+    if (blk == 0) offsets[E] = run;
   }
   __syncthreads();
-  for (int x = threadIdx.x; x < E; x += blockDim.x) counts[x] = totals[x];
-  for (int x = threadIdx.x; x <= E; x += blockDim.x) offsets[x] = offs[x];
-  for (int64_t i = threadIdx.x; i < nblk * E; i += blockDim.x) blk_base[i] += offs[i % E];
-}
 
-__global__ __launch_bounds__(256) void route_scatter_kernel(const int32_t* __restrict__ expert_id,
-                                                            int E, int64_t T,
-                                                            const int32_t* __restrict__ blk_base,
-                                                            int32_t* __restrict__ perm,
-                                                            int32_t* __restrict__ inv_perm) {
-  __shared__ int cnt[kChunks][kMaxE];
-  __shared__ int pre[kChunks][kMaxE];
-  const int lane = threadIdx.x & 63;
-  const int wave = threadIdx.x >> 6;
-  const int64_t base = (int64_t)blockIdx.x * kTokPerBlock;
   const uint64_t below = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
-  int my_e[4], my_rank[4];
+  const int64_t b0 = (int64_t)blk * tpb;
+  const int64_t b1 = min(T, b0 + tpb);
+  for (int64_t r0 = b0; r0 < b1; r0 += kRound) {
+    int my_e[4], my_rank[4];
 #pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    const int c = wave * 4 + j;
-    const int64_t t = base + c * kWave + lane;
-    const int e = (t < T) ? expert_id[t] : -1;
-    int rank = 0;
-    for (int x = 0; x < E; ++x) {
-      const uint64_t m = __ballot(e == x);
-      if (e == x) rank = __popcll(m & below);
-      if (lane == 0) cnt[c][x] = __popcll(m);
+    for (int j = 0; j < 4; ++j) {
+      const int64_t t = r0 + (wave * 4 + j) * kWave + lane;
+      my_e[j] = t < b1 ? expert_id[t] : -1;
     }
-    my_e[j] = e;
-    my_rank[j] = rank;
-  }
-  __syncthreads();
-  for (int x = threadIdx.x; x < E; x += blockDim.x) {
-    int s = blk_base[(int64_t)blockIdx.x * E + x];
 #pragma unroll
-    for (int c = 0; c < kChunks; ++c) {
-      pre[c][x] = s;
-      s += cnt[c][x];
+    for (int j = 0; j < 4; ++j) {
+      const int c = wave * 4 + j;
+      int rank = 0;
+      for (int x = 0; x < E; ++x) {
+        const uint64_t m = __ballot(my_e[j] == x);
+        if (my_e[j] == x) rank = __popcll(m & below);
+        if (lane == 0) cnt[c][x] = __popcll(m);
+      }
+      my_rank[j] = rank;
     }
-  }
-  __syncthreads();
+    __syncthreads();
+    for (int x = threadIdx.x; x < E; x += blockDim.x) {
+      int s = base[x];
 #pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    const int c = wave * 4 + j;
-    const int64_t t = base + c * kWave + lane;
-    if (t < T) {
-      const int pos = pre[c][my_e[j]] + my_rank[j];
-      perm[pos] = (int32_t)t;
-      inv_perm[t] = pos;
+      for (int c = 0; c < kChunks; ++c) {
+        pre[c][x] = s;
+        s += cnt[c][x];
+      }
+      base[x] = s;
     }
+    __syncthreads();
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int64_t t = r0 + (wave * 4 + j) * kWave + lane;
+      if (t < b1) {
+        const int pos = pre[wave * 4 + j][my_e[j]] + my_rank[j];
+        perm[pos] = (int32_t)t;
+        inv_perm[t] = pos;
+      }
+    }
+    __syncthreads();  // cnt / pre are rewritten by the next round
   }
 }
 
-// out[i] = in[perm[i]] (gather) or out[perm[i]] = in[i] (scatter); one wave per row.
+// Both launches of a plan; blk_counts holds nblk * E ints.
+int route_plan_launch(const int64_t* ids, int64_t T, const int64_t* map, int64_t V, int32_t E, int32_t* expert_id,
+                      int32_t* perm, int32_t* inv_perm, int32_t* counts, int32_t* offsets, int32_t* blk_counts,
+                      hipStream_t s, const char* name) {
+  const int64_t tpb = tokens_per_block(T);
+  const int nblk = (int)((T + tpb - 1) / tpb);
+  if (nblk > 0) {
+    route_count_kernel<<<dim3((unsigned)nblk), dim3(256), 0, s>>>(ids, map, V, E, T, tpb, expert_id, blk_counts);
+    if (int rc = check_launch(name)) return rc;
+  }
+  // At least one block: with T == 0 it writes the zero counts and offsets.
+  route_scatter_kernel<<<dim3((unsigned)(nblk > 0 ? nblk : 1)), dim3(256), 0, s>>>(
+      expert_id, E, T, tpb, nblk, blk_counts, perm, inv_perm, counts, offsets);
+  return check_launch(name);
+}
+
+int route_plan_check(const int64_t* ids, int64_t T, const int64_t* map, int64_t V, int32_t E, int32_t* expert_id,
+                     int32_t* perm, int32_t* inv_perm, int32_t* counts, int32_t* offsets, const char* name) {
+  if (T < 0 || T > INT32_MAX) return fail(CDX_EINVAL, "%s: T=%lld out of range", name, (long long)T);
+  if (E <= 0 || E > kMaxE) return fail(CDX_EUNSUPPORTED, "%s: E=%d must be in [1, %d]", name, E, kMaxE);
+  if (map != nullptr && V <= 0) return fail(CDX_EINVAL, "%s: V=%lld must be > 0", name, (long long)V);
+  if (!counts || !offsets) return fail(CDX_EINVAL, "%s: null counts/offsets", name);
+  if (T > 0 && (!ids || !expert_id || !perm || !inv_perm))
+    return fail(CDX_EINVAL, "%s: null ids/expert_id/perm/inv_perm", name);
+  return CDX_OK;
+}
+
+// out[i] = in[perm[i]] (gather) or out[perm[i]] = in[i] (scatter).  HBM-bound: one
+// wave per row, each lane moving up to kPermVec 16-byte vectors of it with all its
+// loads issued before its stores; both sides are streamed (non-temporal), as no row
+// is read twice.  A permutation entry outside [0, T) copies nothing.
+constexpr int kPermVec = 4;
+
 template <bool GATHER>
 __global__ __launch_bounds__(256) void permute_rows_kernel(const uint4* __restrict__ in,
                                                            const int32_t* __restrict__ perm,
                                                            int64_t T, int64_t vec_per_row,
                                                            uint4* __restrict__ out) {
+  typedef __attribute__((ext_vector_type(4))) unsigned int u32x4_t;
   const int lane = threadIdx.x & 63;
   const int64_t i = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
   if (i >= T) return;
   const int64_t p = perm[i];
-  const uint4* src = in + (GATHER ? p : i) * vec_per_row;
-  uint4* dst = out + (GATHER ? i : p) * vec_per_row;
-  for (int64_t v = lane; v < vec_per_row; v += kWave) dst[v] = src[v];
+  if (p < 0 || p >= T) return;
+  const u32x4_t* src = reinterpret_cast<const u32x4_t*>(in + (GATHER ? p : i) * vec_per_row);
+  u32x4_t* dst = reinterpret_cast<u32x4_t*>(out + (GATHER ? i : p) * vec_per_row);
+  for (int64_t v0 = 0; v0 < vec_per_row; v0 += kPermVec * kWave) {
+    u32x4_t r[kPermVec];
+#pragma unroll
+    for (int u = 0; u < kPermVec; ++u) {
+      const int64_t v = v0 + u * kWave + lane;
+      if (v < vec_per_row) r[u] = __builtin_nontemporal_load(src + v);
+    }
+#pragma unroll
+    for (int u = 0; u < kPermVec; ++u) {
+      const int64_t v = v0 + u * kWave + lane;
+      if (v < vec_per_row) __builtin_nontemporal_store(r[u], dst + v);
+    }
+  }
 }
 
 }  // namespace
 }  // namespace cdx
 
 extern "C" size_t cdx_route_workspace_bytes(int64_t T, int32_t E) {
-  if (T < 0 || E <= 0) return 0;
-  const int64_t nblk = (T + cdx::kTokPerBlock - 1) / cdx::kTokPerBlock;
-  return (size_t)(2 * nblk * E) * sizeof(int32_t);
+  if (T <= 0 || E <= 0) return 0;
+  const int64_t tpb = cdx::tokens_per_block(T);
+  return (size_t)(((T + tpb - 1) / tpb) * E) * sizeof(int32_t);
 }
 
 extern "C" int cdx_route_plan(const int64_t* ids, int64_t T, const int64_t* map, int64_t V,
@@ -209,30 +257,13 @@ extern "C" int cdx_route_plan(const int64_t* ids, int64_t T, const int64_t* map,
                               size_t workspace_bytes, void* stream) {
   using namespace cdx;
   clear_error();
-  if (T < 0 || T > INT32_MAX) return fail(CDX_EINVAL, "cdx_route_plan: T=%lld out of range", (long long)T);
-  if (E <= 0 || E > kMaxE) return fail(CDX_EUNSUPPORTED, "cdx_route_plan: E=%d must be in [1, %d]", E, kMaxE);
-  if (map != nullptr && V <= 0) return fail(CDX_EINVAL, "cdx_route_plan: V=%lld must be > 0", (long long)V);
-  if (!counts || !offsets) return fail(CDX_EINVAL, "cdx_route_plan: null counts/offsets");
-  if (T > 0 && (!ids || !expert_id || !perm || !inv_perm))
-    return fail(CDX_EINVAL, "cdx_route_plan: null ids/expert_id/perm/inv_perm");
+  const char* name = "cdx_route_plan";
+  if (int rc = route_plan_check(ids, T, map, V, E, expert_id, perm, inv_perm, counts, offsets, name)) return rc;
   const size_t need = cdx_route_workspace_bytes(T, E);
   if (need > 0 && (workspace == nullptr || workspace_bytes < need))
-    return fail(CDX_EWORKSPACE, "cdx_route_plan: workspace needs %zu bytes, got %zu", need, workspace_bytes);
-  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
-  const int64_t nblk = (T + kTokPerBlock - 1) / kTokPerBlock;
-  int32_t* blk_counts = static_cast<int32_t*>(workspace);
-  int32_t* blk_base = blk_counts + nblk * E;
-  if (nblk > 0) {
-    route_count_kernel<<<dim3((unsigned)nblk), dim3(256), 0, s>>>(ids, map, V, E, T, expert_id, blk_counts);
-    if (int rc = check_launch("cdx_route_plan/count")) return rc;
-  }
-  route_scan_kernel<<<dim3(1), dim3(1024), 0, s>>>(nblk, E, blk_counts, blk_base, counts, offsets);
-  if (int rc = check_launch("cdx_route_plan/scan")) return rc;
-  if (nblk > 0) {
-    route_scatter_kernel<<<dim3((unsigned)nblk), dim3(256), 0, s>>>(expert_id, E, T, blk_base, perm, inv_perm);
-    if (int rc = check_launch("cdx_route_plan/scatter")) return rc;
-  }
-  return CDX_OK;
+    return fail(CDX_EWORKSPACE, "%s: workspace needs %zu bytes, got %zu", name, need, workspace_bytes);
+  return route_plan_launch(ids, T, map, V, E, expert_id, perm, inv_perm, counts, offsets,
+                           static_cast<int32_t*>(workspace), reinterpret_cast<hipStream_t>(stream), name);
 }
 
 static int permute_common(const void* in, const int32_t* perm, int64_t T, int64_t row_bytes,

@@ -87,3 +87,15 @@ def test_permute_roundtrip_and_sort_api(cdx, oracle):
     back = unpermute_rows(sorted_x, perm)
     assert torch.equal(back, x)
     assert torch.equal(permute_rows(x, perm), sorted_x)
+
+
+@pytest.mark.parametrize("T,E", [(256 * 1024, 64), (256 * 1024 + 1, 8), (300_000, 64), (1_000_003, 5)])
+def test_plan_large_token_counts(cdx, oracle, T, E):
+    """Token counts at and past 256 blocks of 1024, where each block walks several
+    rounds of 1024 tokens; random ids over a 32000 map, E up to 64."""
+    print(f"route plan large T={T} E={E}", flush=True)
+    g = torch.Generator().manual_seed(T)
+    ids = torch.randint(0, 32000, (T,), generator=g)
+    tmap = torch.randint(0, E, (32000,), generator=g)
+    plan = cdx.route_plan(ids.cuda(), tmap.cuda(), E)
+    _check(plan, oracle.route_plan(ids.numpy(), tmap.numpy(), E))
