@@ -35,6 +35,17 @@ def _weight(weight: torch.Tensor, like: torch.Tensor) -> torch.Tensor:
     return weight if weight.is_contiguous() else weight.contiguous()
 
 
+def _check_out(t: Optional[torch.Tensor], x: torch.Tensor, what: str) -> None:
+    """A caller-provided output must be a contiguous tensor of x's shape, dtype and device:
+    the kernel writes T * H values through its base pointer."""
+    if t is None:
+        return
+    if t.shape != x.shape or t.dtype != x.dtype or t.device != x.device or not t.is_contiguous():
+        raise ValueError(f"add_rms_norm: {what} must be a contiguous {x.dtype} tensor of shape "
+                         f"{tuple(x.shape)} on {x.device}, got {tuple(t.shape)} {t.dtype} on {t.device}"
+                         f"{'' if t.is_contiguous() else ' (not contiguous)'}")
+
+
 def add_rms_norm(x: torch.Tensor, residual: Optional[torch.Tensor], weight: torch.Tensor,
                  eps: float = 1e-6, *, out: Optional[torch.Tensor] = None,
                  residual_out: Optional[torch.Tensor] = None,
@@ -56,6 +67,8 @@ def add_rms_norm(x: torch.Tensor, residual: Optional[torch.Tensor], weight: torc
     w = _weight(weight, x2)
     if w.numel() != H:
         raise ValueError(f"add_rms_norm: weight has {w.numel()} elements, hidden size is {H}")
+    _check_out(out, x, "out")
+    _check_out(residual_out, x, "residual_out")
     y = out if out is not None else torch.empty(shape, dtype=x.dtype, device=x.device)
     h = None
     if residual is not None and store_residual:

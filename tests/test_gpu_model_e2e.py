@@ -1,0 +1,170 @@
+"""End-to-end GPU forwards of the benchmark models, against the fp32 oracle.
+
+* Configuration 1, the reference README's model (README.md:66-84): hidden 768, 18
+  layers, 12 Q / 4 KV heads, intermediate 2048, 4 routed experts + shared expert, mu
+  guidance, vocab 32000, seed 0; batch 4 x seq 512 Zipf(1.1) ids with the greedy
+  bin-packed map.  The whole batch is compared.
+* Configuration 4, the 1B preset (hidden 2048, 24 layers, 16 / 8 heads, intermediate
+  5632, 8 experts + shared), seed 1; the full 8 x 2048 batch runs on the GPU and its
+  first whole sequence is compared (the fp32 oracle takes a few seconds per 2048
+  tokens on the host).
+
+The oracle receives the GPU model's own bf16 weights in fp32.  A forward stacks many
+bf16 roundings, so the bound is the model-level one of tests/test_gpu_model.py:
+normwise max rel err <= 3e-2 and relative RMS <= 2e-2 on the logits.
+
+Also here: the reference's ablation pattern (run_ablations.py:45-78, mu_to_q/k/v
+weights zeroed and restored through ``.data``) replayed after a forward; no host
+synchronisation inside a warm forward (SURVEY 3.4's contract, checked with torch's
+sync debug mode); and a bf16-cast attention layer at S = 2048 against the oracle,
+which pins the RoPE angles at long positions.
+"""
+
+from __future__ import annotations
+
+import pytest
+import torch
+
+from _metrics import errors
+
+pytestmark = pytest.mark.gpu
+MODEL_MAX_REL = 3e-2
+MODEL_REL_RMS = 2e-2
+
+
+def _build(cdx, cfg, seed, device=None):
+    from complexity_deep import synthetic as syn
+    torch.manual_seed(seed)
+    if device is not None:
+        with torch.device(device):
+            m = cdx.ComplexityModel(cfg)
+    else:
+        m = cdx.ComplexityModel(cfg)
+    syn.install_expert_map(m, syn.binpacked_map(cfg.vocab_size, cfg.num_experts))
+    return m.to("cuda", torch.bfloat16).eval()
+
+
+def _fp32_state(m):
+    return {k: v.detach().float().cpu() for k, v in m.state_dict().items()}
+
+
+def _check(logits, ref, what):
+    e = errors(logits, ref)
+    print(f"{what}: {e}", flush=True)
+    assert e["max_rel"] <= MODEL_MAX_REL and e["rel_rms"] <= MODEL_REL_RMS, (what, e)
+
+
+def readme_config(cdx):
+    return cdx.ComplexityConfig(vocab_size=32000, hidden_size=768, intermediate_size=2048, num_hidden_layers=18,
+                                num_attention_heads=12, num_key_value_heads=4, num_experts=4, shared_expert=True,
+                                use_mu_guidance=True)
+
+
+def test_cfg1_readme_model_forward(cdx, oracle):
+    from complexity_deep import synthetic as syn
+    print("cfg1 README model, 4 x 512", flush=True)
+    cfg = readme_config(cdx)
+    m = _build(cdx, cfg, seed=0)
+    ids = syn.zipf_token_ids(4, 512, cfg.vocab_size, seed=0)
+    with torch.no_grad():
+        logits = m(ids.cuda()).logits.float().cpu()
+    assert logits.shape == (4, 512, cfg.vocab_size)
+    with torch.no_grad():
+        ref = oracle.forward(_fp32_state(m), cfg.to_dict(), ids)
+    _check(logits, ref, "cfg1 logits")
+
+
+def test_cfg4_1b_forward(cdx, oracle):
+    from complexity_deep import synthetic as syn
+    print("cfg4 1B model, 8 x 2048 (sequence 0 checked)", flush=True)
+    cfg = cdx.ComplexityConfig.complexity_1b()
+    cfg.vocab_size = 32000
+    m = _build(cdx, cfg, seed=1, device="cuda")
+    ids = syn.zipf_token_ids(8, 2048, cfg.vocab_size, seed=1)
+    with torch.no_grad():
+        logits = m(ids.cuda()).logits
+    assert logits.shape == (8, 2048, cfg.vocab_size)
+    seq0 = logits[:1].float().cpu()
+    assert torch.isfinite(logits).all()
+    sd = _fp32_state(m)
+    del logits, m
+    torch.cuda.empty_cache()
+    with torch.no_grad():
+        ref = oracle.forward(sd, cfg.to_dict(), ids[:1])
+    _check(seq0, ref, "cfg4 logits, sequence 0")
+
+
+def _small(cdx):
+    return cdx.ComplexityConfig(vocab_size=2048, hidden_size=256, intermediate_size=704, num_hidden_layers=3,
+                                num_attention_heads=4, num_key_value_heads=2, num_experts=4)
+
+
+def test_mu_ablation_replay_after_forward(cdx, oracle):
+    """run_ablations.py:45-78: weights zeroed with .data.zero_() after a forward and
+    restored with .data.copy_(); the forward must follow both writes."""
+    from complexity_deep import synthetic as syn
+    print("mu ablation replay", flush=True)
+    cfg = _small(cdx)
+    m = _build(cdx, cfg, seed=3)
+    ids = syn.zipf_token_ids(2, 128, cfg.vocab_size, seed=3).cuda()
+    with torch.inference_mode():
+        base = m(ids).logits.clone()
+    saved = {}
+    for name, mod in m.named_modules():
+        for attr in ("mu_to_k", "mu_to_q", "mu_to_v"):
+            if hasattr(mod, attr):
+                saved[(name, attr)] = getattr(mod, attr).weight.data.clone()
+                getattr(mod, attr).weight.data.zero_()
+    assert saved
+    with torch.inference_mode():
+        ablated = m(ids).logits.clone()
+    ref = oracle.forward(_fp32_state(m), cfg.to_dict(), ids.cpu())  # the zeroed weights
+    _check(ablated.float().cpu(), ref, "ablated logits")
+    assert not torch.equal(ablated, base), "zeroing the mu weights must change the output"
+    for (name, attr), w in saved.items():
+        getattr(m.get_submodule(name), attr).weight.data.copy_(w)
+    with torch.inference_mode():
+        restored = m(ids).logits
+    assert torch.equal(restored, base), "restoring the weights must give the first output bit for bit"
+
+
+def test_forward_has_no_host_sync(cdx):
+    from complexity_deep import synthetic as syn
+    print("no host sync in a warm forward", flush=True)
+    cfg = _small(cdx)
+    m = _build(cdx, cfg, seed=4)
+    ids = syn.zipf_token_ids(2, 256, cfg.vocab_size, seed=4).cuda()
+    with torch.inference_mode():
+        m(ids)  # first call: weight bindings, map grouping, RoPE tables
+        torch.cuda.synchronize()
+        torch.cuda.set_sync_debug_mode("error")
+        try:
+            out = m(ids).logits
+        finally:
+            torch.cuda.set_sync_debug_mode("default")
+    torch.cuda.synchronize()
+    assert torch.isfinite(out).all()
+
+
+def test_bf16_attention_long_positions(cdx, oracle):
+    """A bf16-cast attention layer at S = 2048 (cast rounds the inv_freq buffer; the
+    RoPE tables must still follow the fp32 constructor angles) against the oracle."""
+    print("bf16 attention S=2048", flush=True)
+    B, S, H, nq, nkv = 1, 2048, 1024, 8, 4
+    torch.manual_seed(5)
+    attn = cdx.ComplexityAttention(H, nq, nkv, max_position_embeddings=2048)
+    with torch.no_grad():
+        for n in ("q_norm", "k_norm"):
+            getattr(attn, n).weight.uniform_(0.5, 1.5)
+    attn = attn.to("cuda", torch.bfloat16).eval()
+    g = torch.Generator().manual_seed(6)
+    x = torch.randn(B, S, H, generator=g).to(torch.bfloat16)
+    mu = torch.randn(B, S, H, generator=g).clamp(-2, 2).to(torch.bfloat16)
+    with torch.no_grad():
+        out, _ = attn(x.cuda(), mu_prev=mu.cuda())
+    sd = {"a." + k: v.float().cpu() for k, v in attn.state_dict().items()}
+    cfg = {"num_attention_heads": nq, "num_key_value_heads": nkv, "use_qk_norm": True, "rope_theta": 10000.0}
+    ref = oracle.attention(x.float(), mu.float(), sd, "a.", cfg)
+    e = errors(out, ref)
+    print(f"bf16 attention S=2048: {e}", flush=True)
+    assert e["max_rel"] <= 2e-2 and e["rel_rms"] <= 1e-2, e

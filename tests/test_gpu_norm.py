@@ -86,3 +86,23 @@ def test_reference_operator_api(cdx, oracle):
         m.weight.copy_(w)
         o3, r3b = m(x3, r3)
     assert torch.equal(o3, out) and torch.equal(r3b, res)
+
+
+def test_out_buffers_are_checked(cdx):
+    """Caller-provided out / residual_out must be contiguous bf16 tensors of x's shape
+    on x's device: the kernel writes T * H values through their base pointers."""
+    from complexity_deep.normalization import add_rms_norm
+    x = torch.randn(8, 256, device="cuda").to(bf16)
+    r = torch.randn(8, 256, device="cuda").to(bf16)
+    w = torch.ones(256, device="cuda", dtype=bf16)
+    bad = [torch.empty(8, 128, device="cuda", dtype=bf16),           # shape
+           torch.empty(8, 256, device="cuda", dtype=torch.float32),  # dtype
+           torch.empty(256, 8, device="cuda", dtype=bf16).t(),       # not contiguous
+           torch.empty(8, 256, dtype=bf16)]                          # device
+    for t in bad:
+        with pytest.raises(ValueError, match="out must be"):
+            add_rms_norm(x, r, w, out=t)
+        with pytest.raises(ValueError, match="residual_out must be"):
+            add_rms_norm(x, r, w, residual_out=t)
+    y, h = add_rms_norm(x, r, w, out=torch.empty_like(x), residual_out=r)
+    assert h.data_ptr() == r.data_ptr()
