@@ -31,6 +31,8 @@ _SIGNATURES = {
     "cdx_route_workspace_bytes": (ctypes.c_size_t, [_i64, _i32]),
     "cdx_route_plan": (ctypes.c_int, [_vp, _i64, _vp, _i64, _i32, _vp, _vp, _vp, _vp, _vp, _vp,
                                       ctypes.c_size_t, _vp]),
+    "cdx_route_noalloc_scratch_bytes": (ctypes.c_size_t, []),
+    "cdx_route_plan_noalloc": (ctypes.c_int, [_vp, _i64, _vp, _i64, _i32, _vp, _vp, _vp, _vp, _vp, _vp]),
     "cdx_permute_rows": (ctypes.c_int, [_vp, _vp, _i64, _i64, _vp, _vp]),
     "cdx_unpermute_rows": (ctypes.c_int, [_vp, _vp, _i64, _i64, _vp, _vp]),
     "cdx_moe_swiglu_fwd": (ctypes.c_int, [_vp, _i64, _i32, _i32, _i32, _i32, _vp, _vp, _vp, _vp, _vp,

@@ -266,6 +266,61 @@ extern "C" int cdx_route_plan(const int64_t* ids, int64_t T, const int64_t* map,
                            static_cast<int32_t*>(workspace), reinterpret_cast<hipStream_t>(stream), name);
 }
 
+// ---- allocation-free variant --------------------------------------------------
+// The count table of cdx_route_plan_noalloc lives in this file-scope device array,
+// one copy per GPU, held until the process ends.  In host code the name `scratch`
+// denotes a host-side shadow, not device memory: the device address is looked up
+// once per device (hipGetSymbolAddress with that device current) and only that
+// address is ever handed to a kernel.  Calls on one GPU share the array, so calls
+// that overlap in time on one GPU (different streams, or host threads) race; calls
+// ordered on one stream do not.  Nothing in it needs clearing between calls: the
+// count launch writes every entry the scatter launch then reads.
+static __device__ __align__(256) int32_t scratch[cdx::kScratchInts];
+
+namespace {
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+int32_t* g_scratch_dev[kMaxDevices] = {};
+
+// Device address of `scratch` on the current device (looked up on first use).
+int scratch_on_current_device(int32_t** out, const char* name) {
+  int dev = -1;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0)
+    return cdx::fail(CDX_ELAUNCH, "%s: hipGetDevice failed", name);
+  if (dev >= kMaxDevices) return cdx::fail(CDX_EUNSUPPORTED, "%s: device %d >= %d", name, dev, kMaxDevices);
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (g_scratch_dev[dev] == nullptr) {
+    void* p = nullptr;
+    const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || p == nullptr)
+      return cdx::fail(CDX_ELAUNCH, "%s: hipGetSymbolAddress(scratch) failed on device %d: %s", name, dev,
+                       hipGetErrorString(e));
+    g_scratch_dev[dev] = static_cast<int32_t*>(p);
+  }
+  *out = g_scratch_dev[dev];
+  return CDX_OK;
+}
+}  // namespace
+
+extern "C" size_t cdx_route_noalloc_scratch_bytes(void) { return sizeof(scratch); }
+
+extern "C" int cdx_route_plan_noalloc(const int64_t* ids, int64_t T, const int64_t* map, int64_t V, int32_t E,
+                                      int32_t* expert_id, int32_t* perm, int32_t* inv_perm, int32_t* counts,
+                                      int32_t* offsets, void* stream) {
+  using namespace cdx;
+  clear_error();
+  const char* name = "cdx_route_plan_noalloc";
+  if (int rc = route_plan_check(ids, T, map, V, E, expert_id, perm, inv_perm, counts, offsets, name)) return rc;
+  const size_t need = cdx_route_workspace_bytes(T, E);
+  if (need > sizeof(scratch))
+    return fail(CDX_EWORKSPACE, "%s: the count table needs %zu bytes, the library scratch holds %zu", name, need,
+                sizeof(scratch));
+  int32_t* table = nullptr;
+  if (int rc = scratch_on_current_device(&table, name)) return rc;
+  return route_plan_launch(ids, T, map, V, E, expert_id, perm, inv_perm, counts, offsets, table,
+                           reinterpret_cast<hipStream_t>(stream), name);
+}
+
 static int permute_common(const void* in, const int32_t* perm, int64_t T, int64_t row_bytes,
                           void* out, void* stream, bool gather, const char* name) {
   using namespace cdx;

@@ -95,6 +95,27 @@ int cdx_route_plan(const int64_t* ids_dev, int64_t T, const int64_t* map_dev, in
                    void* workspace_dev, size_t workspace_bytes, void* stream);
 
 /*
+ * cdx_route_plan without a workspace argument and without any allocation: the
+ * per-block count table lives in a library-owned device array of
+ * cdx_route_noalloc_scratch_bytes() bytes (64 KB: 256 blocks x 64 experts of int32),
+ * one per GPU, held until the process ends.  Outputs and limits as cdx_route_plan
+ * (E <= 64, T <= 2^31 - 1); a plan whose table would not fit is rejected with
+ * CDX_EWORKSPACE.  The array's device address is looked up on the first call on each
+ * device, which must then be the current device.  All calls on one GPU share the
+ * array: calls that overlap in time on one GPU (two streams, two host threads) race
+ * and must be ordered by the caller; calls on one stream are ordered already.
+ *
+ * No counterpart in the reference: this entry point exists for callers that cannot
+ * allocate device memory (code under HIP graph capture, tight serving loops,
+ * harnesses that forbid hipMalloc).
+ */
+size_t cdx_route_noalloc_scratch_bytes(void);
+int cdx_route_plan_noalloc(const int64_t* ids_dev, int64_t T, const int64_t* map_dev, int64_t V,
+                           int32_t E, int32_t* expert_id_dev, int32_t* perm_dev,
+                           int32_t* inv_perm_dev, int32_t* counts_dev, int32_t* offsets_dev,
+                           void* stream);
+
+/*
  * Row gather / scatter by a permutation (rows of `row_bytes` bytes, a multiple of 16):
  *   permute:    out[i]       = in[perm[i]]
  *   unpermute:  out[perm[i]] = in[i]
