@@ -306,11 +306,8 @@ __global__ __launch_bounds__(kGemmThreads, Cfg::MINB) void gemm_nt_kernel(const 
       AL == ALoad::kConcat ? (uintptr_t)(p.a2 + m0 * p.lda2) - (uintptr_t)p.k_split * 2 : a_base;
   // kSegmented: the A descriptor covers the tile's rows only, so that a masked row's
   // offset (kMaskedOff) reads zeros; each row remembers its expert (-1 past m_end).
-  // kGather: it covers the M source rows, so that a permutation entry outside them
-  // reads zeros instead of leaving the operand (the host bounds M * lda to 4 GB).
   const __amdgpu_buffer_rsrc_t rs_a =
       AL == ALoad::kSegmented ? make_rsrc((const void*)a_base, (uint32_t)((m_end - m0) * p.lda * 2))
-      : AL == ALoad::kGather  ? make_rsrc((const void*)a_base, (uint32_t)(p.M * p.lda * 2))
                               : make_rsrc((const void*)a_base);
   const __amdgpu_buffer_rsrc_t rs_b = make_rsrc(bexp + (int64_t)n0 * p.ldb);
   const uintptr_t b_base = (uintptr_t)(bexp + (int64_t)n0 * p.ldb);
@@ -334,8 +331,13 @@ __global__ __launch_bounds__(kGemmThreads, Cfg::MINB) void gemm_nt_kernel(const 
     }
     gm = gm < m_end ? gm : m_end - 1;  // rows past the segment are loaded but never stored
     if (AL == ALoad::kGather) {
-      const int64_t src = p.perm[gm];
-      a_off[j] = (src < 0 || src >= p.M) ? kMaskedOff : (uint32_t)((src * p.lda + dchunk * 8) * 2);
+      // A permutation entry outside [0, M) is clamped into it (negative entries wrap
+      // to large unsigned values first): a corrupt permutation reads wrong rows but
+      // stays inside the operand.  The host bounds M * lda * 2 to 4 GB.  (This kernel
+      // runs at the register limit: a select here pushed the compiler into moving
+      // values through AGPRs inside the K loop.)
+      const uint32_t src = min((uint32_t)p.perm[gm], (uint32_t)(p.M - 1));
+      a_off[j] = (src * (uint32_t)p.lda + (uint32_t)dchunk * 8u) * 2u;
     } else {
       a_off[j] = (uint32_t)(((gm - m0) * p.lda + dchunk * 8) * 2);
     }

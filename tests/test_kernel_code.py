@@ -1,0 +1,56 @@
+"""CPU checks of the generated gfx950 code of the MFMA tile engine.
+
+The GEMM kernels hold 256 fp32 accumulators per lane in AGPRs and run close to the
+256-VGPR limit.  A small source change can tip the register allocator into moving
+values between VGPRs and AGPRs (v_accvgpr_read / v_accvgpr_write) or into scratch
+inside the K loop, which costs 20-30 % of the kernel's time without changing any
+result; a range check on permutation entries once did exactly that to the MoE
+gate/up pass.  This test compiles cdx_gemm.hip to assembly (hipcc, no GPU needed)
+and checks that the K loop of every engine instantiation is free of both and holds
+the expected MFMA count per iteration (two K32 sub-steps of 8 x 8 blocks).
+"""
+
+from __future__ import annotations
+
+import re
+import subprocess
+from pathlib import Path
+
+import pytest
+
+REPO = Path(__file__).resolve().parents[1]
+HIPCC = "/opt/rocm/bin/hipcc"
+
+
+@pytest.fixture(scope="module")
+def gemm_asm(tmp_path_factory):
+    if not Path(HIPCC).exists():
+        pytest.skip("hipcc not available")
+    out = tmp_path_factory.mktemp("asm") / "cdx_gemm.s"
+    cmd = [HIPCC, "--offload-arch=gfx950", "-O3", "-std=c++17", "-fPIC", "-Xclang", "-target-feature", "-Xclang",
+           "-packed-fp32-ops", "--cuda-device-only", "-S", str(REPO / "complexity-deep_amd/csrc/cdx_gemm.hip"),
+           "-o", str(out)]
+    subprocess.run(cmd, check=True, capture_output=True)
+    return out.read_text()
+
+
+def _main_loops(asm: str):
+    for name in re.findall(r"^(_ZN3cdx14gemm_nt_kernel\S+):", asm, re.M):
+        start = asm.index(name + ":")
+        body = asm[start:asm.index(".Lfunc_end", start)]
+        loops = [m.group(1) for m in re.finditer(r"^\.LBB\d+_\d+:[^\n]*Loop Header[^\n]*\n(.*?)(?=^\.LBB|\Z)",
+                                                 body, re.M | re.S) if "v_mfma" in m.group(1)]
+        yield name, loops
+
+
+def test_gemm_k_loops_have_no_register_shuffles(gemm_asm):
+    seen = 0
+    for name, loops in _main_loops(gemm_asm):
+        assert len(loops) == 1, f"{name}: expected one MFMA loop, found {len(loops)}"
+        loop = loops[0]
+        seen += 1
+        assert loop.count("v_mfma_f32_16x16x32_bf16") == 128, name
+        assert "v_accvgpr_read" not in loop and "v_accvgpr_write" not in loop, \
+            f"{name}: VGPR/AGPR shuffles inside the K loop"
+        assert "scratch_" not in loop and "buffer_store" not in loop, f"{name}: spills inside the K loop"
+    assert seen >= 10
