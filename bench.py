@@ -10,18 +10,27 @@ from Zipf(1.1), with the greedy bin-packed expert map installed in every layer a
 random-normal weights (seed 1).  A step is one forward returning logits; `value` is
 tokens per second with inputs already in HBM.
 
-The other workloads run one hot-path piece on its own (for profiling):
-  "moe-layer"     configuration 2: TokenRoutedMLP, 16384 x 768, E=4, Ie=512 + shared
-  "qkv-norm"      configuration 3: add+RMSNorm then mu-QKV, 32768 x 2048, 16q/8kv x 128
-  "route-stress"  configuration 5: routing plan + MoE layer, 65536 tokens, 90% skew
+The other workloads run one configuration each:
+  "readme-forward"  configuration 1: the reference README's model (hidden 768, 18
+                    layers, 12/4 heads, E=4 + shared), batch 4 x seq 512, seed 0
+  "moe-layer"       configuration 2: TokenRoutedMLP, 16384 x 768, E=4, Ie=512 + shared
+  "qkv-norm"        configuration 3: add+RMSNorm then mu-QKV, 32768 x 2048, 16q/8kv x 128
+  "route-stress"    configuration 5: routing plan + MoE layer, 65536 tokens, 90% skew
+  "route-permute"   configuration 5's token rows (65536 x 2048 bf16) permuted into
+                    expert order and back (cdx_permute_rows / cdx_unpermute_rows)
+After the headline workload (and its CPU baselines) the default run also times each
+of these for a few steps and reports them under "workloads" (skip: --no-extras).
 
 Printed: ONE JSON line on stdout.  Besides the contract keys it carries
   roofline      the dominant hot-path kernel's achieved rate against the MI355X peak
                 (2.5 PFLOP/s dense bf16 MFMA, 8 TB/s HBM), from HIP events recorded
-                around each launch on the stream it runs on, over the timed steps;
+                around each launch on the stream it runs on, over a second pass of
+                the timed steps;
   kernels       the same for every hot-path entry point;
   cpu_baseline  the fp32 CPU restatement (oracle/) timed on this host over a bounded
-                sample of the same workload, plus its agreement with the GPU logits.
+                sample of the same workload, plus its agreement with the GPU logits;
+                under "readme_forward" the same for configuration 1's whole batch;
+  workloads     per extra workload: tokens/s, ms per step, roofline and kernels.
 Everything else goes to stderr.
 """
 
@@ -94,8 +103,16 @@ def work_of(name: str, s: dict):
         # ids in; one table row read and one output row written per token
         return float(s["T"] * (8 + 2 * 2 * s["H"])), "byte"
     if name == "route_plan":
-        # ids in; expert_id, perm, inv_perm out; the map is read once per token at most
-        return float(s["T"] * (8 + 4 + 4 + 4) + 2 * 4 * (s["E"] + 1)), "byte"
+        # ids in; expert_id, perm, inv_perm out; the map is read once per token at most.
+        # A few hundred KB in two launches: bound by launch latency, not by HBM.
+        return float(s["T"] * (8 + 4 + 4 + 4) + 2 * 4 * (s["E"] + 1)), "latency"
+    if name in ("permute_rows", "unpermute_rows"):
+        # every row read once and written once (plus the int32 permutation)
+        return float(s["T"] * (2 * s["row_bytes"] + 4)), "byte"
+    if name == "swiglu":
+        return float(3 * s["n"] * s["elt"]), "byte"
+    if name == "grouped_gemm":
+        return 2.0 * s["T"] * s["K"] * s["N"], "flop"
     return 0.0, "none"
 
 
@@ -134,6 +151,8 @@ class KernelTimer:
                 gbs = a["work"] / (a["ms"] * 1e-3) / 1e9
                 rec.update(bound="hbm", achieved=round(gbs, 1), unit="GB/s",
                            frac=round(gbs / PEAK_HBM_GBS, 4), work_per_launch=a["work"] / a["calls"])
+            elif a["kind"] == "latency":
+                rec.update(bound="launch latency", bytes_per_launch=a["work"] / a["calls"])
             out[name] = rec
         return out
 
@@ -178,6 +197,55 @@ def workload_1b(args, dev):
               "weights": "random normal init (std 0.02, residual 0.02/sqrt(48)), seed 1, cast to bf16",
               "parallelism": "single GPU"}
     return step, T, config, ("mu_qkv",), (cfg, model, ids_cpu)
+
+
+def build_readme(dev):
+    import torch
+    import complexity_deep as cd
+    from complexity_deep import synthetic as syn
+    cfg = cd.ComplexityConfig(vocab_size=32000, hidden_size=768, intermediate_size=2048, num_hidden_layers=18,
+                              num_attention_heads=12, num_key_value_heads=4, num_experts=4, shared_expert=True,
+                              use_mu_guidance=True)
+    torch.manual_seed(0)
+    model = cd.ComplexityModel(cfg)
+    syn.install_expert_map(model, syn.binpacked_map(cfg.vocab_size, cfg.num_experts))
+    ids = syn.zipf_token_ids(4, 512, cfg.vocab_size, seed=0)
+    return cfg, model, ids
+
+
+def workload_readme(args, dev):
+    import torch
+    cfg, model, ids_cpu = build_readme(dev)
+    model = model.to(dev, torch.bfloat16).eval()
+    ids = ids_cpu.to(dev)
+
+    def step():
+        return model(ids).logits
+
+    config = {"workload": "configuration 1: the reference README model forward (logits)", "hidden": 768,
+              "layers": 18, "heads_q_kv_dim": [12, 4, 64], "intermediate": 2048, "experts": 4, "shared_expert": True,
+              "vocab": 32000, "global_batch": 4, "seq_len": 512, "tokens_per_step": ids.numel(),
+              "token_ids": "Zipf(1.1) over 32000, seed 0", "expert_map": "greedy bin-packing of the Zipf pmf",
+              "weights": "random normal init (std 0.02, residual 0.02/sqrt(36)), seed 0, cast to bf16"}
+    return step, ids.numel(), config, ("mu_qkv",), None
+
+
+def workload_route_permute(args, dev):
+    import torch
+    from complexity_deep import synthetic as syn
+    from complexity_deep.token_routed_mlp import permute_rows, route_plan, unpermute_rows
+    T, H, E = 65536, 2048, 8
+    tmap = syn.binpacked_map(32000, E)
+    ids = syn.routing_stress_ids(T, tmap, E, heavy=1, seed=0).to(dev)
+    x = syn.normal_bf16((T, H), seed=2, device=dev)
+    plan = route_plan(ids, tmap.to(dev), E)
+
+    def step():
+        return unpermute_rows(permute_rows(x, plan.perm), plan.perm)
+
+    config = {"workload": "configuration 5 token rows permuted into expert order and back", "tokens_per_step": T,
+              "row_bytes": 2 * H, "token_ids": "90% heavy expert 1, 1% each other, rest id 0, seed 0"}
+    return step, T, config, ("permute_rows", "unpermute_rows"), None
 
 
 def workload_moe(args, dev):
@@ -251,8 +319,10 @@ def workload_route_stress(args, dev):
     return step, T, config, ("moe_swiglu", "route_plan"), None
 
 
-WORKLOADS = {"1b-forward": workload_1b, "moe-layer": workload_moe, "qkv-norm": workload_qkv_norm,
-             "route-stress": workload_route_stress}
+WORKLOADS = {"1b-forward": workload_1b, "readme-forward": workload_readme, "moe-layer": workload_moe,
+             "qkv-norm": workload_qkv_norm, "route-stress": workload_route_stress,
+             "route-permute": workload_route_permute}
+EXTRAS = ("readme-forward", "moe-layer", "qkv-norm", "route-stress", "route-permute")
 
 
 # ---------------------------------------------------------------------------
@@ -270,6 +340,12 @@ def cpu_model_name() -> str:
     return platform.processor() or "unknown"
 
 
+def _logit_agreement(gpu, ref):
+    d = gpu.float().cpu() - ref
+    return {"max_rel": float(d.abs().max() / ref.abs().max()),
+            "rel_rms": float(d.pow(2).mean().sqrt() / ref.pow(2).mean().sqrt())}
+
+
 def cpu_baseline_1b(ctx, gpu_logits0, seqs: int):
     import torch
     from oracle import oracle as orc
@@ -284,19 +360,98 @@ def cpu_baseline_1b(ctx, gpu_logits0, seqs: int):
         ref = orc.forward(sd, cfg.to_dict(), sample)
         dt = time.perf_counter() - t0
     tok = sample.numel()
-    d = gpu_logits0[:seqs].float().cpu() - ref
-    max_rel = float(d.abs().max() / ref.abs().max())
-    rel_rms = float(d.pow(2).mean().sqrt() / ref.pow(2).mean().sqrt())
+    agree = _logit_agreement(gpu_logits0[:seqs], ref)
     log(f"cpu baseline: {tok} tokens in {dt:.2f} s ({tok / dt:.1f} tok/s, {threads} threads); "
-        f"GPU logits vs CPU fp32: max_rel={max_rel:.3e} rel_rms={rel_rms:.3e}")
+        f"GPU logits vs CPU fp32: max_rel={agree['max_rel']:.3e} rel_rms={agree['rel_rms']:.3e}")
     return {"value": round(tok / dt, 2), "unit": "tokens/s", "cores": threads, "kind": "port",
             "sample": f"{seqs} x 2048 tokens (the first {seqs} sequence(s) of the workload batch), the full "
                       f"24-layer 1B forward in fp32 through oracle.forward (torch CPU, {threads} threads)",
             "seconds": round(dt, 3), "cpu_model": cpu_model_name(), "affinity_cores": len(os.sched_getaffinity(0)),
-            "gpu_vs_cpu_logits": {"max_rel": max_rel, "rel_rms": rel_rms}}
+            "gpu_vs_cpu_logits": agree}
+
+
+def cpu_baseline_readme(dev):
+    """Configuration 1 (the reference README model, 4 x 512 tokens) through the fp32
+    oracle on this host, and the same batch through the bf16 GPU model for agreement
+    and for the GPU rate of the same workload."""
+    import torch
+    from oracle import oracle as orc
+    cfg, model, ids = build_readme(dev)
+    # the oracle sees the bf16-rounded weights the GPU model holds
+    sd = {k: (v.detach().to(torch.bfloat16).float() if v.is_floating_point() else v.detach())
+          for k, v in model.state_dict().items()}
+    threads = torch.get_num_threads()
+    with torch.no_grad():
+        orc.forward(sd, cfg.to_dict(), ids[:1, :64])  # warm-up
+        t0 = time.perf_counter()
+        ref = orc.forward(sd, cfg.to_dict(), ids)
+        dt = time.perf_counter() - t0
+    gpu_model = model.to(dev, torch.bfloat16).eval()
+    with torch.inference_mode():
+        logits = gpu_model(ids.to(dev)).logits
+    agree = _logit_agreement(logits, ref)
+    tok = ids.numel()
+    log(f"cpu baseline (configuration 1): {tok} tokens in {dt:.2f} s ({tok / dt:.1f} tok/s, {threads} threads); "
+        f"GPU logits vs CPU fp32: max_rel={agree['max_rel']:.3e} rel_rms={agree['rel_rms']:.3e}")
+    return {"value": round(tok / dt, 2), "unit": "tokens/s", "cores": threads, "kind": "port",
+            "sample": f"configuration 1 whole: the README model (768 hidden, 18 layers, E=4 + shared) over "
+                      f"4 x 512 Zipf tokens in fp32 through oracle.forward (torch CPU, {threads} threads)",
+            "seconds": round(dt, 3), "gpu_vs_cpu_logits": agree}
 
 
 # ---------------------------------------------------------------------------
+
+def roofline_of(kernels: dict, dominant, workload: str):
+    dom = next((d for d in dominant if d in kernels), None)
+    if dom is None:
+        return None
+    k = kernels[dom]
+    traffic = measured_traffic(workload)
+    return {"kernel": dom, "bound": k["bound"], "achieved": k["achieved"],
+            "peak": PEAK_BF16_TFLOPS if k["bound"] == "mfma" else PEAK_HBM_GBS,
+            "unit": k["unit"], "frac": k["frac"], "traffic": traffic.get(dom),
+            "traffic_source": f"profiles/hbm_traffic_{workload.replace('-', '_')}.json" if dom in traffic else None,
+            "work_per_launch": k["work_per_launch"], "avg_launch_us": k["avg_us"],
+            "timing": "HIP events around each launch on its stream, over a second pass of the same K steps "
+                      "run right after the timed (event-free) pass"}
+
+
+def run(step, steps: int, warmup: int, kernel_timing: bool):
+    """Warm-up, then `steps` timed steps bracketed by synchronisations (no events in
+    them), then the same steps again with events around every launch."""
+    import torch
+    from complexity_deep import _native as nat
+    timer = KernelTimer()
+    with torch.inference_mode():
+        out = None
+        for _ in range(warmup):
+            out = step()
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(steps):
+            out = step()
+        torch.cuda.synchronize()
+        t1 = time.perf_counter()
+        if kernel_timing:
+            # A second pass of the same K steps with a pair of HIP events around every
+            # launch, kept out of the timed pass (the events cost about 1 ms of GPU
+            # time per 1B step).
+            nat.set_launch_hook(timer)
+            timer.active = True
+            for _ in range(steps):
+                step()
+            torch.cuda.synchronize()
+            timer.active = False
+            nat.set_launch_hook(None)
+    kernels = timer.summary(steps) if kernel_timing else {}
+    return out, t1 - t0, kernels
+
+
+def log_kernels(kernels: dict):
+    for name, k in sorted(kernels.items()):
+        log(f"  {name:14s} {k['launches_per_step']:5.1f}/step avg {k['avg_us']:9.2f} us  "
+            f"{k.get('achieved', 0):9.1f} {k.get('unit', '')}  frac {k.get('frac', 0):.3f}")
+
 
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
@@ -304,9 +459,11 @@ def main() -> int:
     ap.add_argument("--steps", type=int, default=10)
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--workload", choices=sorted(WORKLOADS), default="1b-forward")
-    ap.add_argument("--no-cpu-baseline", action="store_true", help="skip the CPU oracle timing")
+    ap.add_argument("--no-cpu-baseline", action="store_true", help="skip the CPU oracle timings")
     ap.add_argument("--cpu-seqs", type=int, default=1, help="sequences of 2048 tokens in the CPU sample")
     ap.add_argument("--no-kernel-timing", action="store_true", help="do not record per-launch events")
+    ap.add_argument("--no-extras", action="store_true", help="time only the selected workload")
+    ap.add_argument("--extra-steps", type=int, default=10, help="timed steps of each extra workload")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="first run one plain 1 GiB device copy (read 1 GiB, write 1 GiB): the reference "
                          "dispatch that scales FETCH_SIZE / WRITE_SIZE counter runs")
@@ -335,62 +492,42 @@ def main() -> int:
         del src, dst
     log(f"device: {torch.cuda.get_device_name(dev)}; workload {args.workload}")
     step, tokens, config, dominant, ctx = WORKLOADS[args.workload](args, dev)
-
-    timer = KernelTimer()
-    with torch.inference_mode():
-        for i in range(args.warmup):
-            out = step()
-        torch.cuda.synchronize()
-        log(f"warm-up done ({args.warmup} steps)")
-        t0 = time.perf_counter()
-        for _ in range(args.steps):
-            out = step()
-        torch.cuda.synchronize()
-        t1 = time.perf_counter()
-        if not args.no_kernel_timing:
-            # Per-kernel timing: a second pass of the same K steps with a pair of HIP
-            # events around every launch.  Kept out of the headline pass because the
-            # events themselves cost about 1 ms of GPU time per 1B step.
-            nat.set_launch_hook(timer)
-            timer.active = True
-            for _ in range(args.steps):
-                step()
-            torch.cuda.synchronize()
-            timer.active = False
-            nat.set_launch_hook(None)
-    elapsed = t1 - t0
+    out, elapsed, kernels = run(step, args.steps, args.warmup, not args.no_kernel_timing)
     ms = 1e3 * elapsed / args.steps
     value = tokens * args.steps / elapsed
     log(f"timed {args.steps} steps: {ms:.3f} ms/step, {value:.1f} tokens/s")
-
-    kernels = timer.summary(args.steps) if not args.no_kernel_timing else {}
+    log_kernels(kernels)
     hot_ms = sum(k["ms_per_step"] for k in kernels.values())
-    for name, k in sorted(kernels.items()):
-        log(f"  {name:12s} {k['launches_per_step']:5.1f}/step avg {k['avg_us']:9.2f} us  "
-            f"{k.get('achieved', 0):9.1f} {k.get('unit', '')}  frac {k.get('frac', 0):.3f}")
-    roofline = None
-    dom = next((d for d in dominant if d in kernels), None)
-    if dom is not None:
-        k = kernels[dom]
-        traffic = measured_traffic(args.workload)
-        roofline = {"kernel": dom, "bound": k["bound"], "achieved": k["achieved"],
-                    "peak": PEAK_BF16_TFLOPS if k["bound"] == "mfma" else PEAK_HBM_GBS,
-                    "unit": k["unit"], "frac": k["frac"], "traffic": traffic.get(dom),
-                    "traffic_source": f"profiles/hbm_traffic_{args.workload.replace('-', '_')}.json"
-                    if dom in traffic else None,
-                    "work_per_launch": k["work_per_launch"], "avg_launch_us": k["avg_us"],
-                    "timing": "HIP events around each launch on its stream, over a second pass of the same K steps run right after the timed (event-free) pass"}
+    roofline = roofline_of(kernels, dominant, args.workload)
 
     cpu = None
     if args.workload == "1b-forward" and not args.no_cpu_baseline:
         cpu = cpu_baseline_1b(ctx, out, args.cpu_seqs)
+        cpu["readme_forward"] = cpu_baseline_readme(dev)
+    del step, out, ctx
+    torch.cuda.empty_cache()
+
+    workloads = {}
+    if not args.no_extras and args.workload == "1b-forward":
+        for name in EXTRAS:
+            w_step, w_tokens, w_config, w_dom, _ = WORKLOADS[name](args, dev)
+            _, w_elapsed, w_kernels = run(w_step, args.extra_steps, 2, True)
+            w_ms = 1e3 * w_elapsed / args.extra_steps
+            log(f"workload {name}: {w_ms:.3f} ms/step, {w_tokens * args.extra_steps / w_elapsed:.1f} tokens/s")
+            log_kernels(w_kernels)
+            workloads[name] = {"value": round(w_tokens * args.extra_steps / w_elapsed, 1), "unit": "tokens/s",
+                               "ms_per_step": round(w_ms, 4), "steps": args.extra_steps, "warmup": 2,
+                               "config": w_config, "roofline": roofline_of(w_kernels, w_dom, name),
+                               "kernels": w_kernels}
+            del w_step
+            torch.cuda.empty_cache()
 
     rec = {"metric": METRIC, "value": round(value, 1), "unit": "tokens/s", "n_gpus": 1, "steps": args.steps,
            "warmup": args.warmup, "ms_per_step": round(ms, 4), "higher_is_better": True, "scaling": "weak",
            "vs_baseline": None, "dtype": "bf16", "data": "synthetic", "config": config,
            "roofline": roofline, "cpu_baseline": cpu,
            "kernels": kernels, "hot_path_ms_per_step": round(hot_ms, 4),
-           "device": torch.cuda.get_device_name(dev)}
+           "workloads": workloads, "device": torch.cuda.get_device_name(dev)}
     print(json.dumps(rec), flush=True)
     return 0
 

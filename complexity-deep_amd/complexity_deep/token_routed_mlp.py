@@ -86,23 +86,31 @@ def route_plan(ids: torch.Tensor, token_map: Optional[torch.Tensor], num_experts
     return RoutePlan(expert_id, perm, inv_perm, counts, offsets, num_experts)
 
 
+def _aligned_rows(t: torch.Tensor) -> torch.Tensor:
+    """Contiguous with a 16-byte aligned base (the kernels' DMA needs both)."""
+    t = t.contiguous()
+    return t if t.data_ptr() % 16 == 0 else t.clone()
+
+
 def permute_rows(x: torch.Tensor, perm: torch.Tensor) -> torch.Tensor:
     """out[i] = x[perm[i]] for a 2-D tensor (cdx_permute_rows)."""
-    x = x.contiguous()
+    x = _aligned_rows(x)
     out = torch.empty_like(x)
-    nat.check(nat.lib().cdx_permute_rows(x.data_ptr(), perm.data_ptr(), x.shape[0],
-                                         x.shape[1] * x.element_size(), out.data_ptr(),
-                                         nat.stream_of(x)), "cdx_permute_rows")
+    rb = x.shape[1] * x.element_size()
+    with nat.launch_region("permute_rows", x.device, T=x.shape[0], row_bytes=rb):
+        nat.check(nat.lib().cdx_permute_rows(x.data_ptr(), perm.data_ptr(), x.shape[0], rb, out.data_ptr(),
+                                             nat.stream_of(x)), "cdx_permute_rows")
     return out
 
 
 def unpermute_rows(x: torch.Tensor, perm: torch.Tensor) -> torch.Tensor:
     """out[perm[i]] = x[i] for a 2-D tensor (cdx_unpermute_rows)."""
-    x = x.contiguous()
+    x = _aligned_rows(x)
     out = torch.empty_like(x)
-    nat.check(nat.lib().cdx_unpermute_rows(x.data_ptr(), perm.data_ptr(), x.shape[0],
-                                           x.shape[1] * x.element_size(), out.data_ptr(),
-                                           nat.stream_of(x)), "cdx_unpermute_rows")
+    rb = x.shape[1] * x.element_size()
+    with nat.launch_region("unpermute_rows", x.device, T=x.shape[0], row_bytes=rb):
+        nat.check(nat.lib().cdx_unpermute_rows(x.data_ptr(), perm.data_ptr(), x.shape[0], rb, out.data_ptr(),
+                                               nat.stream_of(x)), "cdx_unpermute_rows")
     return out
 
 
@@ -137,12 +145,6 @@ def _offsets_i32(expert_offsets: torch.Tensor, E: int, device: torch.device) -> 
     # Values are not inspected on the host (that would synchronise): the kernels read
     # them clamped to [0, rows], and rows outside [offsets[0], offsets[E]) stay zero.
     return offs.to(device=device, dtype=torch.int32).contiguous()
-
-
-def _aligned_rows(t: torch.Tensor) -> torch.Tensor:
-    """Contiguous with a 16-byte aligned base (the kernels' DMA needs both)."""
-    t = t.contiguous()
-    return t if t.data_ptr() % 16 == 0 else t.clone()
 
 
 def cggr_grouped_gemm(sorted_tokens: torch.Tensor, expert_weights: torch.Tensor,
