@@ -552,6 +552,32 @@ __global__ __launch_bounds__(kGemmThreads, Cfg::MINB) void gemm_nt_kernel(const 
   static_assert(4 * WM * OUT_ROWB <= kStages * STAGE_BYTES, "epilogue staging must fit the LDS");
   __syncthreads();  // every wave is done with the pipeline's LDS stages
   uint8_t* ep = lds + wave * (WM * OUT_ROWB);
+  // Scatter epilogues: the output row of every store-loop iteration (perm) and, for
+  // kScatterAdd, every residual piece this lane adds to are loaded up front, before
+  // the accumulators are staged, so that the two dependent load latencies (perm, then
+  // the residual row) run under the staging instead of after it (loads interleaved
+  // with the stores below would wait one by one: a store may alias a later row's
+  // load).
+  // Rows past the segment and columns past N read a clamped, valid piece (never
+  // stored): guarded loads would become branches, each waiting for its load.
+  constexpr int NIT = WM / RPI;  // store-loop iterations per lane
+  constexpr bool kScatterRows = EP == Epi::kScatter || EP == Epi::kScatterAdd;
+  int32_t prow[kScatterRows ? NIT : 1];
+  uint4 resid[EP == Epi::kScatterAdd ? NIT : 1];
+  if constexpr (kScatterRows) {
+#pragma unroll
+    for (int i = 0; i < NIT; ++i) {
+      const int64_t gm = m0 + wm * WM + i * RPI + lane / OUT_CH;
+      // Clamped into [0, M): a corrupt permutation scrambles rows but stays in C.
+      const int32_t pr = p.perm[gm < m_end ? gm : m_end - 1];
+      prow[i] = pr < 0 ? 0 : (pr >= (int32_t)p.M ? (int32_t)p.M - 1 : pr);
+    }
+  }
+  if constexpr (EP == Epi::kScatterAdd) {
+    const int n = min(n0 + wn * WN + (lane % OUT_CH) * 8, p.N - 8);
+#pragma unroll
+    for (int i = 0; i < NIT; ++i) resid[i] = *reinterpret_cast<const uint4*>(p.c + (int64_t)prow[i] * p.ldc + n);
+  }
   auto stage4 = [&](int r, int col, float y0, float y1, float y2, float y3) __attribute__((always_inline)) {
     uint2 o;
     o.x = pack_bf16x2(y0, y1);
@@ -788,30 +814,6 @@ __global__ __launch_bounds__(kGemmThreads, Cfg::MINB) void gemm_nt_kernel(const 
   // in order; the wait also keeps the compiler from reordering them).  The outputs
   // are streamed (non-temporal stores), which keeps the operands' panels in L2.
   __builtin_amdgcn_s_waitcnt(waitcnt_imm(63, 0));
-  // Scatter epilogues: the output row of every store-loop iteration (perm) and, for
-  // kScatterAdd, every residual piece this lane adds to are loaded up front, once the
-  // accumulators are staged and their registers free (loads interleaved with the
-  // stores below would wait one by one: a store may alias a later row's load).
-  // Rows past the segment and columns past N read a clamped, valid piece (never
-  // stored): guarded loads would become branches, each waiting for its load.
-  constexpr int NIT = WM / RPI;  // store-loop iterations per lane
-  constexpr bool kScatterRows = EP == Epi::kScatter || EP == Epi::kScatterAdd;
-  int32_t prow[kScatterRows ? NIT : 1];
-  uint4 resid[EP == Epi::kScatterAdd ? NIT : 1];
-  if constexpr (kScatterRows) {
-#pragma unroll
-    for (int i = 0; i < NIT; ++i) {
-      const int64_t gm = m0 + wm * WM + i * RPI + lane / OUT_CH;
-      // Clamped into [0, M): a corrupt permutation scrambles rows but stays in C.
-      const int32_t pr = p.perm[gm < m_end ? gm : m_end - 1];
-      prow[i] = pr < 0 ? 0 : (pr >= (int32_t)p.M ? (int32_t)p.M - 1 : pr);
-    }
-  }
-  if constexpr (EP == Epi::kScatterAdd) {
-    const int n = min(n0 + wn * WN + (lane % OUT_CH) * 8, p.N - 8);
-#pragma unroll
-    for (int i = 0; i < NIT; ++i) resid[i] = *reinterpret_cast<const uint4*>(p.c + (int64_t)prow[i] * p.ldc + n);
-  }
   if constexpr (EP == Epi::kQKRope) {
     if (vt_fast) {
       // V^T rows: 16 lanes per 256-byte row, four rows per instruction.
