@@ -248,6 +248,29 @@ def workload_route_permute(args, dev):
     return step, T, config, ("permute_rows", "unpermute_rows"), None
 
 
+def workload_rmsnorm(args, dev):
+    """The 1B forward's plain RMSNorm (16384 x 2048 bf16), 49 launches per step as in one
+    forward, over 8 distinct inputs (537 MB, more than the 256 MB last-level cache) so
+    that every launch reads its input from HBM."""
+    import torch
+    from complexity_deep import synthetic as syn
+    from complexity_deep.normalization import rms_norm
+    T, H, n_in = 16384, 2048, 8
+    xs = [syn.normal_bf16((T, H), seed=10 + i, device=dev) for i in range(n_in)]
+    w = torch.ones(H, dtype=torch.bfloat16, device=dev)
+
+    def step():
+        out = None
+        for i in range(49):
+            out = rms_norm(xs[i % n_in], w, 1e-6)
+        return out
+
+    config = {"workload": "configuration 4's plain RMSNorm: 49 back-to-back launches of 16384 x 2048 bf16 per step, "
+                          "inputs rotating over 8 buffers (537 MB)", "tokens_per_step": 49 * T, "hidden": H,
+              "region_timed": "rmsnorm"}
+    return step, 49 * T, config, ("rmsnorm",), None
+
+
 def workload_moe(args, dev):
     import torch
     import complexity_deep as cd
@@ -321,8 +344,8 @@ def workload_route_stress(args, dev):
 
 WORKLOADS = {"1b-forward": workload_1b, "readme-forward": workload_readme, "moe-layer": workload_moe,
              "qkv-norm": workload_qkv_norm, "route-stress": workload_route_stress,
-             "route-permute": workload_route_permute}
-EXTRAS = ("readme-forward", "moe-layer", "qkv-norm", "route-stress", "route-permute")
+             "route-permute": workload_route_permute, "rmsnorm-1b": workload_rmsnorm}
+EXTRAS = ("readme-forward", "moe-layer", "qkv-norm", "route-stress", "route-permute", "rmsnorm-1b")
 
 
 # ---------------------------------------------------------------------------
@@ -418,7 +441,9 @@ def roofline_of(kernels: dict, dominant, workload: str):
 
 def run(step, steps: int, warmup: int, kernel_timing: bool):
     """Warm-up, then `steps` timed steps bracketed by synchronisations (no events in
-    them), then the same steps again with events around every launch."""
+    them), then the same steps again with events around every launch.  Also returns
+    the GPU time of the timed pass from a pair of HIP events around it (on the
+    current stream, which every entry point launches on)."""
     import torch
     from complexity_deep import _native as nat
     timer = KernelTimer()
@@ -427,11 +452,16 @@ def run(step, steps: int, warmup: int, kernel_timing: bool):
         for _ in range(warmup):
             out = step()
         torch.cuda.synchronize()
+        r0 = torch.cuda.Event(enable_timing=True)
+        r1 = torch.cuda.Event(enable_timing=True)
         t0 = time.perf_counter()
+        r0.record()
         for _ in range(steps):
             out = step()
+        r1.record()
         torch.cuda.synchronize()
         t1 = time.perf_counter()
+        region_ms = r0.elapsed_time(r1)
         if kernel_timing:
             # A second pass of the same K steps with a pair of HIP events around every
             # launch, kept out of the timed pass (the events cost about 1 ms of GPU
@@ -444,7 +474,7 @@ def run(step, steps: int, warmup: int, kernel_timing: bool):
             timer.active = False
             nat.set_launch_hook(None)
     kernels = timer.summary(steps) if kernel_timing else {}
-    return out, t1 - t0, kernels
+    return out, t1 - t0, kernels, region_ms
 
 
 def log_kernels(kernels: dict):
@@ -492,7 +522,7 @@ def main() -> int:
         del src, dst
     log(f"device: {torch.cuda.get_device_name(dev)}; workload {args.workload}")
     step, tokens, config, dominant, ctx = WORKLOADS[args.workload](args, dev)
-    out, elapsed, kernels = run(step, args.steps, args.warmup, not args.no_kernel_timing)
+    out, elapsed, kernels, _ = run(step, args.steps, args.warmup, not args.no_kernel_timing)
     ms = 1e3 * elapsed / args.steps
     value = tokens * args.steps / elapsed
     log(f"timed {args.steps} steps: {ms:.3f} ms/step, {value:.1f} tokens/s")
@@ -511,8 +541,22 @@ def main() -> int:
     if not args.no_extras and args.workload == "1b-forward":
         for name in EXTRAS:
             w_step, w_tokens, w_config, w_dom, _ = WORKLOADS[name](args, dev)
-            _, w_elapsed, w_kernels = run(w_step, args.extra_steps, 2, True)
+            _, w_elapsed, w_kernels, w_region_ms = run(w_step, args.extra_steps, 2, True)
             w_ms = 1e3 * w_elapsed / args.extra_steps
+            rt = w_config.get("region_timed")
+            if rt in w_kernels:
+                # Back-to-back launches of one kernel: its rate over the event-timed pass
+                # (no event pair per launch, whose own cost would dominate a 20 us kernel).
+                k = w_kernels[rt]
+                n = k["launches_per_step"] * args.extra_steps
+                avg_us = 1e3 * w_region_ms / n
+                gbs = k["work_per_launch"] / (avg_us * 1e-6) / 1e9
+                w_kernels[rt + "_region"] = {"launches_per_step": k["launches_per_step"], "avg_us": round(avg_us, 2),
+                                             "bound": "hbm", "achieved": round(gbs, 1), "unit": "GB/s",
+                                             "frac": round(gbs / PEAK_HBM_GBS, 4),
+                                             "work_per_launch": k["work_per_launch"],
+                                             "timing": "HIP events around the whole timed pass / launches"}
+                w_dom = (rt + "_region",) + tuple(w_dom)
             log(f"workload {name}: {w_ms:.3f} ms/step, {w_tokens * args.extra_steps / w_elapsed:.1f} tokens/s")
             log_kernels(w_kernels)
             workloads[name] = {"value": round(w_tokens * args.extra_steps / w_elapsed, 1), "unit": "tokens/s",
