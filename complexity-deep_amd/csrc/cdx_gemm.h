@@ -638,12 +638,23 @@ __global__ __launch_bounds__(kGemmThreads, Cfg::MINB) void gemm_nt_kernel(const 
       const uint16_t* nw = kind == 0 ? q.q_norm_w : (kind == 1 ? q.k_norm_w : nullptr);
       const bool norm = kind != 2 && nw != nullptr;
       // Norm weights of this lane's columns (the same for every row).
+      // Without QK norm the weights are 1 and the scale below is 1: both products are
+      // then exact, and the code has no branch between the norm and the rotation (a
+      // branch there made the compiler pass the values through AGPRs).
       uint2 wpk[BPH];  // 4 bf16 each; one uniform branch around all the loads
 #pragma unroll
-      for (int nb = 0; nb < BPH; ++nb) wpk[nb] = make_uint2(0u, 0u);
+      for (int nb = 0; nb < BPH; ++nb) wpk[nb] = make_uint2(0x3F803F80u, 0x3F803F80u);
       if (norm) {
 #pragma unroll
         for (int nb = 0; nb < BPH; ++nb) wpk[nb] = *reinterpret_cast<const uint2*>(nw + nb * 16 + 4 * q4);
+      }
+      float wf[BPH][4];  // the same weights in fp32, unpacked once for all rows
+#pragma unroll
+      for (int nb = 0; nb < BPH; ++nb) {
+        wf[nb][0] = __uint_as_float(wpk[nb].x << 16);
+        wf[nb][1] = __uint_as_float(wpk[nb].x & 0xffff0000u);
+        wf[nb][2] = __uint_as_float(wpk[nb].y << 16);
+        wf[nb][3] = __uint_as_float(wpk[nb].y & 0xffff0000u);
       }
       // cos / sin of this lane's first-half columns for the rows of block mi, read at
       // the top of the block so that the latency hides behind the norm arithmetic.
@@ -726,23 +737,27 @@ __global__ __launch_bounds__(kGemmThreads, Cfg::MINB) void gemm_nt_kernel(const 
           continue;
         }
         fetch_cs(mi, cs_cur);
-        if (norm) {
-          // RMSNorm over the head: this lane's quarter plus its three partners'.
-          float ss = 0.f;
+        {
+          // RMSNorm over the head: this lane's quarter plus its three partners' (lanes
+          // l ^ 16 through a swizzle, l ^ 32 through v_permlane32_swap, neither of which
+          // touches LDS memory); four independent partial sums keep the chain short.
+          float s4[4] = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
           for (int nb = 0; nb < BPH; ++nb)
 #pragma unroll
-            for (int v = 0; v < 4; ++v) ss += x[nb][v] * x[nb][v];
-          ss += __shfl_xor(ss, 16, 64);
-          ss += __shfl_xor(ss, 32, 64);
-          const float rs = rsqrtf(ss / (float)HD + q.eps);
+            for (int v = 0; v < 4; ++v) s4[v] = __builtin_fmaf(x[nb][v], x[nb][v], s4[v]);
+          float ss = (s4[0] + s4[1]) + (s4[2] + s4[3]);
+          // ds_swizzle bit mode, and-mask 0x1f, xor-mask 0x10: lane l reads lane l ^ 16.
+          ss += __int_as_float(__builtin_amdgcn_ds_swizzle(__float_as_int(ss), 0x401F));
+          const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(ss), __float_as_uint(ss), false, false);
+          ss = __uint_as_float(sw[0]) + __uint_as_float(sw[1]);
+          // ss / HD + eps >= eps > 0 is a normal number: the plain hardware reciprocal
+          // square root needs no denormal scaling.
+          const float rs = norm ? __builtin_amdgcn_rsqf(ss / (float)HD + q.eps) : 1.f;
 #pragma unroll
-          for (int nb = 0; nb < BPH; ++nb) {
-            const float w4[4] = {__uint_as_float(wpk[nb].x << 16), __uint_as_float(wpk[nb].x & 0xffff0000u),
-                                 __uint_as_float(wpk[nb].y << 16), __uint_as_float(wpk[nb].y & 0xffff0000u)};
+          for (int nb = 0; nb < BPH; ++nb)
 #pragma unroll
-            for (int j = 0; j < 4; ++j) x[nb][j] = w4[j] * (x[nb][j] * rs);
-          }
+            for (int j = 0; j < 4; ++j) x[nb][j] = wf[nb][j] * (x[nb][j] * rs);
         }
         if (gm >= m_end) continue;
         // RoPE on each pair (c, c + HALF), c < HALF, sharing the angle of index c:
