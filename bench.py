@@ -18,6 +18,9 @@ The other workloads run one configuration each:
   "route-stress"    configuration 5: routing plan + MoE layer, 65536 tokens, 90% skew
   "route-permute"   configuration 5's token rows (65536 x 2048 bf16) permuted into
                     expert order and back (cdx_permute_rows / cdx_unpermute_rows)
+  "rmsnorm-1b"      configuration 4's plain RMSNorm, 49 launches per step over 8
+                    rotating inputs (every launch reads from HBM; region-timed)
+  "attention-1b"    configuration 4's causal GQA attention core, one layer
 After the headline workload (and its CPU baselines) the default run also times each
 of these for a few steps and reports them under "workloads" (skip: --no-extras).
 
@@ -319,6 +322,24 @@ def workload_qkv_norm(args, dev):
     return step, B * S, config, ("mu_qkv", "add_rmsnorm"), None
 
 
+def workload_attention(args, dev):
+    """Configuration 4's causal GQA attention core, one layer: q [8, 16, 2048, 128] and
+    k / V^T of 8 KV heads, as the fused QKV + RoPE epilogue leaves them."""
+    from complexity_deep import synthetic as syn
+    from complexity_deep.attention import causal_attention, to_vt_layout
+    B, S, nq, nkv, D = 8, 2048, 16, 8, 128
+    q = syn.normal_bf16((B, nq, S, D), seed=1, device=dev)
+    k = syn.normal_bf16((B, nkv, S, D), seed=2, device=dev)
+    vt = to_vt_layout(syn.normal_bf16((B, nkv, S, D), seed=3, device=dev))
+
+    def step():
+        return causal_attention(q, k, vt)
+
+    config = {"workload": "configuration 4's causal GQA attention core (one layer, B 8 x S 2048, 16 q / 8 kv "
+                          "heads of 128)", "tokens_per_step": B * S}
+    return step, B * S, config, ("attention",), None
+
+
 def workload_route_stress(args, dev):
     import torch
     import complexity_deep as cd
@@ -344,8 +365,9 @@ def workload_route_stress(args, dev):
 
 WORKLOADS = {"1b-forward": workload_1b, "readme-forward": workload_readme, "moe-layer": workload_moe,
              "qkv-norm": workload_qkv_norm, "route-stress": workload_route_stress,
-             "route-permute": workload_route_permute, "rmsnorm-1b": workload_rmsnorm}
-EXTRAS = ("readme-forward", "moe-layer", "qkv-norm", "route-stress", "route-permute", "rmsnorm-1b")
+             "route-permute": workload_route_permute, "rmsnorm-1b": workload_rmsnorm,
+             "attention-1b": workload_attention}
+EXTRAS = ("readme-forward", "moe-layer", "qkv-norm", "route-stress", "route-permute", "rmsnorm-1b", "attention-1b")
 
 
 # ---------------------------------------------------------------------------
