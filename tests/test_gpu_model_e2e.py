@@ -8,6 +8,8 @@
   5632, 8 experts + shared), seed 1; the full 8 x 2048 batch runs on the GPU and its
   first whole sequence is compared (the fp32 oracle takes a few seconds per 2048
   tokens on the host).
+* Configuration 5, the routing stress: the same 1B model over 32 x 2048 ids of which
+  90% fall in one expert's vocabulary; sequence 0 is compared.
 
 The oracle receives the GPU model's own bf16 weights in fp32.  A forward stacks many
 bf16 roundings, so the bound is the model-level one of tests/test_gpu_model.py:
@@ -92,6 +94,34 @@ def test_cfg4_1b_forward(cdx, oracle):
     with torch.no_grad():
         ref = oracle.forward(sd, cfg.to_dict(), ids[:1])
     _check(seq0, ref, "cfg4 logits, sequence 0")
+
+
+def test_cfg5_route_stress_forward(cdx, oracle):
+    """Configuration 5 through the whole 1B model: 65536 tokens (32 x 2048) with 90% of
+    the ids in expert 1's vocabulary, 1% in each other expert's and the rest padding id 0,
+    so one routed segment holds most of the batch.  Token rows are independent in the
+    MoE and attention stays inside a sequence, so sequence 0 is checked against the
+    oracle on its own."""
+    from complexity_deep import synthetic as syn
+    print("cfg5 1B model, 32 x 2048 routing-stress ids (sequence 0 checked)", flush=True)
+    cfg = cdx.ComplexityConfig.complexity_1b()
+    cfg.vocab_size = 32000
+    m = _build(cdx, cfg, seed=1, device="cuda")
+    tmap = m.layers[0].mlp.token_to_expert.cpu()
+    ids = syn.routing_stress_ids(32 * 2048, tmap, cfg.num_experts, heavy=1, seed=0).view(32, 2048)
+    counts = torch.bincount(tmap[ids.view(-1)], minlength=cfg.num_experts)
+    assert int(counts[1]) == round(0.9 * ids.numel()), counts  # the heavy expert
+    with torch.no_grad():
+        logits = m(ids.cuda()).logits
+    assert logits.shape == (32, 2048, cfg.vocab_size)
+    assert torch.isfinite(logits).all()
+    seq0 = logits[:1].float().cpu()
+    sd = _fp32_state(m)
+    del logits, m
+    torch.cuda.empty_cache()
+    with torch.no_grad():
+        ref = oracle.forward(sd, cfg.to_dict(), ids[:1])
+    _check(seq0, ref, "cfg5 logits, sequence 0")
 
 
 def _small(cdx):
