@@ -20,7 +20,7 @@ The other workloads run one configuration each:
                     expert order and back (cdx_permute_rows / cdx_unpermute_rows)
   "rmsnorm-1b"      configuration 4's plain RMSNorm, 49 launches per step over 8
                     rotating inputs (every launch reads from HBM; region-timed)
-  "attention-1b"    configuration 4's causal GQA attention core, one layer
+  "attention-1b"    configuration 4's causal GQA attention core, one layer (region-timed)
 After the headline workload (and its CPU baselines) the default run also times each
 of these for a few steps and reports them under "workloads" (skip: --no-extras).
 
@@ -336,7 +336,7 @@ def workload_attention(args, dev):
         return causal_attention(q, k, vt)
 
     config = {"workload": "configuration 4's causal GQA attention core (one layer, B 8 x S 2048, 16 q / 8 kv "
-                          "heads of 128)", "tokens_per_step": B * S}
+                          "heads of 128)", "tokens_per_step": B * S, "region_timed": "attention"}
     return step, B * S, config, ("attention",), None
 
 
@@ -572,10 +572,14 @@ def main() -> int:
                 k = w_kernels[rt]
                 n = k["launches_per_step"] * args.extra_steps
                 avg_us = 1e3 * w_region_ms / n
-                gbs = k["work_per_launch"] / (avg_us * 1e-6) / 1e9
+                rate = k["work_per_launch"] / (avg_us * 1e-6)
+                if k["bound"] == "mfma":
+                    achieved, unit, peak = rate / 1e12, "TFLOP/s", PEAK_BF16_TFLOPS
+                else:
+                    achieved, unit, peak = rate / 1e9, "GB/s", PEAK_HBM_GBS
                 w_kernels[rt + "_region"] = {"launches_per_step": k["launches_per_step"], "avg_us": round(avg_us, 2),
-                                             "bound": "hbm", "achieved": round(gbs, 1), "unit": "GB/s",
-                                             "frac": round(gbs / PEAK_HBM_GBS, 4),
+                                             "bound": k["bound"], "achieved": round(achieved, 1), "unit": unit,
+                                             "frac": round(achieved / peak, 4),
                                              "work_per_launch": k["work_per_launch"],
                                              "timing": "HIP events around the whole timed pass / launches"}
                 w_dom = (rt + "_region",) + tuple(w_dom)
