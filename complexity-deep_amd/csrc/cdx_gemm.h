@@ -687,19 +687,19 @@ __global__ __launch_bounds__(kGemmThreads, Cfg::MINB) void gemm_nt_kernel(const 
           if (vt_fast) {
             // Quad transpose: lanes 4j + t (same q4) hold tokens 4j + t of dims
             // 4 q4 + (0..3); afterwards lane 4j + t holds dim 4 q4 + t of tokens
-            // 4j + (0..3), as two packed bf16 pairs, in two exchange rounds (lane
-            // t ^ 1, then t ^ 2) over the quad.
+            // 4j + (0..3), as two packed bf16 pairs, in two exchanges (lane t ^ 1,
+            // then t ^ 2) over the quad.
             const int t = lane & 3, j = (lane >> 2) & 3;
             const bool odd = t & 1, upper = t & 2;
 #pragma unroll
             for (int nb = 0; nb < BPH; ++nb) {
               const uint32_t p0 = pack_bf16x2(x[nb][0], x[nb][1]), p1 = pack_bf16x2(x[nb][2], x[nb][3]);
-              // round 1: even lanes give dims 1, 3 and keep 0, 2; odd lanes the reverse.
+              // first exchange: even lanes give dims 1, 3 and keep 0, 2; odd lanes the reverse.
               const uint32_t give = __builtin_amdgcn_perm(p1, p0, odd ? 0x05040100u : 0x07060302u);
               const uint32_t got = (uint32_t)__builtin_amdgcn_mov_dpp((int)give, 0xB1, 0xF, 0xF, true);
               const uint32_t a0 = __builtin_amdgcn_perm(got, p0, odd ? 0x03020504u : 0x05040100u);
               const uint32_t a1 = __builtin_amdgcn_perm(got, p1, odd ? 0x03020706u : 0x07060100u);
-              // round 2: lanes t < 2 give their second pair, t >= 2 their first.
+              // second exchange: lanes t < 2 give their second pair, t >= 2 their first.
               const uint32_t give2 = upper ? a0 : a1;
               const uint32_t got2 = (uint32_t)__builtin_amdgcn_mov_dpp((int)give2, 0x4E, 0xF, 0xF, true);
               uint2 w;

@@ -17,8 +17,8 @@ normwise max rel err <= 3e-2 and relative RMS <= 2e-2 on the logits.
 
 Also here: the reference's ablation pattern (run_ablations.py:45-78, mu_to_q/k/v
 weights zeroed and restored through ``.data``) replayed after a forward; no host
-synchronisation inside a warm forward (SURVEY 3.4's contract, checked with torch's
-sync debug mode); and a bf16-cast attention layer at S = 2048 against the oracle,
+synchronisation inside a warm forward (the forward is stream-ordered end to end;
+checked with torch's sync debug mode); and a bf16-cast attention layer at S = 2048 against the oracle,
 which pins the RoPE angles at long positions.
 """
 
