@@ -49,8 +49,6 @@ __device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
   return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, bf16x2_t));
 }
 
-// 16-byte store with the non-temporal hint (streamed output that the kernel does
-// not read back).
 // Eight bf16 sums a + b, each added in fp32 and rounded once (a bf16 tensor add).
 __device__ __forceinline__ uint4 add_bf16x8(const uint4& a, const uint4& b) {
   const uint32_t aw[4] = {a.x, a.y, a.z, a.w}, bw[4] = {b.x, b.y, b.z, b.w};
@@ -63,6 +61,8 @@ __device__ __forceinline__ uint4 add_bf16x8(const uint4& a, const uint4& b) {
   }
   return make_uint4(r[0], r[1], r[2], r[3]);
 }
+// 16-byte store with the non-temporal hint (streamed output that the kernel does
+// not read back).
 __device__ __forceinline__ void store_nt16(void* p, const uint4& v) {
   typedef __attribute__((ext_vector_type(4))) unsigned int u32x4_t;
   const u32x4_t w = {v.x, v.y, v.z, v.w};
