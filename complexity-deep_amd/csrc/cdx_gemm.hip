@@ -11,7 +11,7 @@
 //   cdx_mu_guidance_fwd  mu = clamp(h @ W_mu^T + clamp(mu_param), lo, hi), the
 //                        producer of the next layer's mu operand
 //   cdx_linear_fwd       y = x @ W^T (the tied LM head)
-#include "cdx_gemm.h"
+#include "cdx_gemm_persist.h"
 
 namespace cdx {
 namespace {
@@ -25,6 +25,17 @@ int launch(GemmParams p, hipStream_t s, const char* name) {
   // The kernel's K loop runs at least once and whole steps only.
   if (p.K < Cfg::BK || p.K % Cfg::BK != 0)
     return fail(CDX_EUNSUPPORTED, "%s: K=%d must be a positive multiple of %d", name, p.K, Cfg::BK);
+  // Whole tiles of a plain (unsegmented) product with more tiles than CUs run on the
+  // persistent form: one block per CU (a multiple of 8, so that every XCD's share of
+  // the tiles has blocks) walking its XCD's tiles.
+  if constexpr ((AL == ALoad::kDense || AL == ALoad::kConcat) && (EP == Epi::kStore || EP == Epi::kBiasClamp) &&
+                Cfg::BN == 256) {
+    const int64_t grid = (device_cu_count() + kNumXcd - 1) / kNumXcd * kNumXcd;
+    if (p.offsets == nullptr && p.M % kBM == 0 && p.N % Cfg::BN == 0 && p.K >= 2 * Cfg::BK && nb > grid) {
+      gemm_persist_kernel<Cfg, AL, EP><<<dim3((unsigned)grid), dim3(kGemmThreads), 0, s>>>(p);
+      return check_launch(name);
+    }
+  }
   gemm_nt_kernel<Cfg, AL, EP, HD><<<dim3((unsigned)nb), dim3(kGemmThreads), 0, s>>>(p);
   return check_launch(name);
 }

@@ -1,0 +1,323 @@
+// Persistent form of the MFMA tile engine (cdx_gemm.h) for whole tiles of a dense or
+// concat A operand (M and N multiples of the tile, no expert segments).
+//
+// gemm_nt_kernel runs one tile per block, so every tile pays a block launch, its setup
+// and a prologue that waits for its first K step to arrive from L2 or HBM.  Here a grid
+// of one block per CU walks the tiles of its XCD's range (the same logical order as
+// gemm_nt_kernel: contiguous per XCD, groups of kGroupM M tiles).  The refill issued by
+// a tile's second-to-last K step is the next tile's first step, so that step lands
+// while the tile finishes and writes its results.  The epilogue stages the results
+// through the other LDS stage in two halves of 64 rows per wave (16 KB per wave, one
+// stage in all); the next tile's second step is issued when it is done.  The first K
+// step of a tile starts its accumulators from zero (the MFMA's C operand is the
+// constant 0), so nothing clears them between tiles.
+//
+// K loop, fragment reads, LDS layout, DMA placement and the staged-store layout are
+// those of gemm_nt_kernel.
+#pragma once
+
+#include "cdx_gemm.h"
+
+namespace cdx {
+
+template <class Cfg, ALoad AL, Epi EP>
+__global__ __launch_bounds__(kGemmThreads, 1) void gemm_persist_kernel(const GemmParams p) {
+  static_assert(AL == ALoad::kDense || AL == ALoad::kConcat, "persistent tiles: dense or concat A only");
+  static_assert(EP == Epi::kStore || EP == Epi::kBiasClamp, "persistent tiles: store or bias-clamp epilogue");
+  static_assert(Cfg::STAGES == 2 && Cfg::MINB == 1 && Cfg::BN == 256, "persistent tiles: 256 x 256, two stages");
+  constexpr int kBN = Cfg::BN, kBK = Cfg::BK, kStages = 2;
+  constexpr int ROW_BYTES = kBK * 2;
+  constexpr int CPR = kBK / 8;
+  constexpr int RPL = 256 / ROW_BYTES;
+  constexpr int A_TILE_BYTES = kBM * ROW_BYTES;
+  constexpr int STAGE_BYTES = Cfg::STAGE_BYTES;
+  constexpr int WM = kBM / 2, WN = kBN / 2;
+  constexpr int MI = WM / 16, NI = WN / 16;
+  constexpr int ROWS_PER_DMA = 1024 / ROW_BYTES;
+  constexpr int LD_A = kBM / ROWS_PER_DMA / 4;
+  constexpr int LD_B = kBN / ROWS_PER_DMA / 4;
+  constexpr int LD_PER_STEP = LD_A + LD_B;
+  constexpr int NSUB = kBK / 32;
+  constexpr int NFRAG = MI + NI;
+  constexpr int DMA_EVERY = Cfg::DMA_EVERY, DMA_OFF = Cfg::DMA_OFF, RD_EVERY = Cfg::READ_EVERY;
+  // Epilogue staging: per wave and half, 64 rows of WN bf16 (256 bytes), 16-byte
+  // chunk c of row r at position c ^ (r % 16).
+  constexpr int OUT_ROWB = WN * 2, OUT_CH = OUT_ROWB / 16, HALF_ROWS = WM / 2, RPI = 64 / OUT_CH;
+  static_assert(NSUB == 2, "one K step is two K32 sub-steps");
+  static_assert(4 * HALF_ROWS * OUT_ROWB <= STAGE_BYTES, "a staged half must fit one stage");
+
+  __shared__ __attribute__((aligned(1024))) uint8_t lds[kStages * STAGE_BYTES];
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wm = wave >> 1, wn = wave & 1;
+
+  // ---- this block's tiles ------------------------------------------------------
+  // XCD x (blocks b with b % 8 == x) owns logical tiles [x_first, x_first + x_count);
+  // its k-th block takes tiles x_first + k, x_first + k + x_blocks, ...
+  const int tiles = p.mt_count * p.nt_count;
+  const int xcd = blockIdx.x % kNumXcd, kx = blockIdx.x / kNumXcd;
+  const int tq = tiles / kNumXcd, tr = tiles % kNumXcd;
+  const int x_first = xcd < tr ? xcd * (tq + 1) : tr * (tq + 1) + (xcd - tr) * tq;
+  const int x_count = tq + (xcd < tr ? 1 : 0);
+  const int x_blocks = (int)(gridDim.x / kNumXcd) + (xcd < (int)(gridDim.x % kNumXcd) ? 1 : 0);
+  if (kx >= x_count) return;
+
+  // Tile i of the XCD's range: first row and column and the DMA bases (A rows and B
+  // rows of the tile; concat: also the mu and mu-weight sources, k_split columns before
+  // their first column, so that both K halves take the scalar offset 2 k0).  Separate
+  // scalars: a struct selected through a reference ends up in scratch memory.
+  auto tile_at = [&](int i, int64_t& m0, int& n0, uintptr_t& a, uintptr_t& a2, uintptr_t& b, uintptr_t& b2)
+                     __attribute__((always_inline)) {
+    const int L = x_first + i;
+    const int per_group = kGroupM * p.nt_count;
+    const int group = L / per_group;
+    const int first_m = group * kGroupM;
+    const int gsz = min(p.mt_count - first_m, kGroupM);
+    const int in_group = L - group * per_group;
+    m0 = (int64_t)__builtin_amdgcn_readfirstlane(first_m + in_group % gsz) * kBM;
+    n0 = __builtin_amdgcn_readfirstlane(in_group / gsz) * kBN;
+    a = (uintptr_t)(p.a + m0 * p.lda);
+    b = (uintptr_t)(p.b + (int64_t)n0 * p.ldb);
+    if constexpr (AL == ALoad::kConcat) {
+      a2 = (uintptr_t)(p.a2 + m0 * p.lda2) - (uintptr_t)p.k_split * 2;
+      b2 = (uintptr_t)(p.b2 + (int64_t)n0 * p.ldb) - (uintptr_t)p.k_split * 2;
+    } else {
+      a2 = a;
+      b2 = b;
+    }
+  };
+
+  // ---- per-lane DMA offsets (the same for every whole tile) ----------------------
+  const int dr = lane / CPR;
+  uint32_t a_off[LD_A], a2_off[LD_A], b_off[LD_B];
+#pragma unroll
+  for (int j = 0; j < LD_A; ++j) {
+    const int r = wave * (kBM / 4) + j * ROWS_PER_DMA + dr;
+    const int dchunk = (lane % CPR) ^ ((r / RPL) % CPR);
+    a_off[j] = (uint32_t)(((int64_t)r * p.lda + dchunk * 8) * 2);
+    a2_off[j] = AL == ALoad::kConcat ? (uint32_t)(((int64_t)r * p.lda2 + dchunk * 8) * 2) : 0u;
+  }
+#pragma unroll
+  for (int j = 0; j < LD_B; ++j) {
+    const int r = wave * (kBN / 4) + j * ROWS_PER_DMA + dr;
+    const int dchunk = (lane % CPR) ^ ((r / RPL) % CPR);
+    b_off[j] = (uint32_t)(((int64_t)r * p.ldb + dchunk * 8) * 2);
+  }
+  const int a_dma_off = wave * (kBM / 4) * ROW_BYTES;
+  const int b_dma_off = A_TILE_BYTES + wave * (kBN / 4) * ROW_BYTES;
+
+  const int KT = p.K / kBK;  // the host guarantees KT >= 2
+  const __amdgpu_buffer_rsrc_t rs_none = make_rsrc(p.b, 0u);
+  int ti = kx;  // index of the current tile in the XCD's range
+  int64_t cur_m0, nxt_m0;
+  int cur_n0, nxt_n0;
+  uintptr_t cur_a, cur_a2, cur_b, cur_b2, nxt_a, nxt_a2, nxt_b, nxt_b2;
+  tile_at(ti, cur_m0, cur_n0, cur_a, cur_a2, cur_b, cur_b2);
+  bool has_next = ti + x_blocks < x_count;
+  tile_at(has_next ? ti + x_blocks : ti, nxt_m0, nxt_n0, nxt_a, nxt_a2, nxt_b, nxt_b2);
+
+  // Where a DMA reads: k0, the current or the next tile, and whether there is one.
+  struct StepSrc {
+    int k0;
+    bool next;
+    bool live;
+  };
+  auto dma1 = [&](const StepSrc st, int stage, int d) __attribute__((always_inline)) {
+    const int k0 = st.k0;
+    const bool second = AL == ALoad::kConcat && k0 >= p.k_split;
+    uint8_t* dst = lds + stage * STAGE_BYTES;
+    if (d < LD_A) {
+      const uintptr_t first_src = st.next ? nxt_a : cur_a, second_src = st.next ? nxt_a2 : cur_a2;
+      const __amdgpu_buffer_rsrc_t r = make_rsrc((const void*)(second ? second_src : first_src));
+      buf_dma16(st.live ? r : rs_none, second ? a2_off[d] : a_off[d], (uint32_t)k0 * 2, dst + a_dma_off + d * 1024);
+    } else {
+      const uintptr_t first_src = st.next ? nxt_b : cur_b, second_src = st.next ? nxt_b2 : cur_b2;
+      const __amdgpu_buffer_rsrc_t r = make_rsrc((const void*)(second ? second_src : first_src));
+      buf_dma16(st.live ? r : rs_none, b_off[d - LD_A], (uint32_t)k0 * 2, dst + b_dma_off + (d - LD_A) * 1024);
+    }
+  };
+  // Refill of step g of the current tile's stream: its own steps, then the next
+  // tile's first step (step KT), fetching nothing after the block's last tile.
+  auto refill_src = [&](int g) __attribute__((always_inline)) {
+    return g < KT ? StepSrc{g * kBK, false, true} : StepSrc{0, true, has_next};
+  };
+
+  // ---- fragments ---------------------------------------------------------------
+  const int fr_row = lane & 15;
+  int fr_off[NSUB];
+#pragma unroll
+  for (int s = 0; s < NSUB; ++s)
+    fr_off[s] = fr_row * ROW_BYTES + (((4 * s + (lane >> 4)) ^ ((fr_row / RPL) % CPR)) << 4);
+  const int a_frag_base = wm * WM * ROW_BYTES;
+  const int b_frag_base = A_TILE_BYTES + wn * WN * ROW_BYTES;
+  bf16x8 fa[2][MI], fb[2][NI];
+  auto read1 = [&](int stage, int s, int set, int f) __attribute__((always_inline)) {
+    const uint8_t* base = lds + stage * STAGE_BYTES;
+    if (f < MI) {
+      fa[set][f] = *reinterpret_cast<const bf16x8*>(base + a_frag_base + f * 16 * ROW_BYTES + fr_off[s]);
+    } else {
+      fb[set][f - MI] = *reinterpret_cast<const bf16x8*>(base + b_frag_base + (f - MI) * 16 * ROW_BYTES + fr_off[s]);
+    }
+  };
+  auto read_frags = [&](int stage, int s, int set) __attribute__((always_inline)) {
+#pragma unroll
+    for (int f = 0; f < NFRAG; ++f) read1(stage, s, set, f);
+  };
+
+  f32x4 acc[MI][NI];
+  // Cleared between tiles.  The empty asm makes the zeros opaque: with them known,
+  // the compiler feeds the first MFMAs a constant C operand and then moves their
+  // results between AGPRs and VGPRs to reach the K loop's registers.
+  auto zero_acc = [&]() __attribute__((always_inline)) {
+#pragma unroll
+    for (int mi = 0; mi < MI; ++mi)
+#pragma unroll
+      for (int ni = 0; ni < NI; ++ni) {
+        acc[mi][ni] = f32x4{0.f, 0.f, 0.f, 0.f};
+        asm volatile("" : "+a"(acc[mi][ni]));
+      }
+  };
+  auto mfma1 = [&](int set, int i, bool first) __attribute__((always_inline)) {
+    const int mi = i / NI, ni = i % NI;
+    (void)first;
+    acc[mi][ni] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(fb[set][ni], fa[set][mi], acc[mi][ni], 0, 0, 0);
+  };
+
+  // ---- K step --------------------------------------------------------------------
+  // Sub-step 0: its MFMAs (from zero accumulators on a tile's first step) with the
+  // fragment reads of sub-step 1 behind them.  Sub-step 1: wait for the next step's
+  // DMA and the barrier, then its MFMAs with the refill of the freed stage (step
+  // kt + 2) and the fragment reads of step kt + 1, both left out on the tile's last
+  // step (its stage then stages the results).
+  auto kstep = [&](int kt, int stage, int next_stage, bool first, bool last) __attribute__((always_inline)) {
+#pragma unroll
+    for (int i = 0; i < MI * NI; ++i) {
+      mfma1(0, i, first);
+      if (i % RD_EVERY == 0 && i / RD_EVERY < NFRAG) read1(stage, 1, 1, i / RD_EVERY);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    const StepSrc st = refill_src(kt + kStages);
+    __builtin_amdgcn_s_waitcnt(waitcnt_imm(0, 0));
+    __syncthreads();
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int i = 0; i < MI * NI; ++i) {
+      mfma1(1, i, false);
+      if (!last && i % DMA_EVERY == DMA_OFF && i / DMA_EVERY < LD_PER_STEP) dma1(st, stage, i / DMA_EVERY);
+      if (!last && i % RD_EVERY == 0 && i / RD_EVERY < NFRAG) read1(next_stage, 0, 0, i / RD_EVERY);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    if (!last) {
+#pragma unroll
+      for (int d = (MI * NI - DMA_OFF + DMA_EVERY - 1) / DMA_EVERY; d < LD_PER_STEP; ++d) dma1(st, stage, d);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+  };
+
+  // ---- epilogue --------------------------------------------------------------------
+  // Lane l holds row l & 15 of each 16 x 16 block and its columns 4 (l >> 4) .. + 3.
+  const int q4 = lane >> 4;
+  const int rl = lane & 15;
+  float4 bias4[EP == Epi::kBiasClamp ? NI : 1];
+  auto load_bias = [&](int n0) __attribute__((always_inline)) {
+    if constexpr (EP == Epi::kBiasClamp) {
+#pragma unroll
+      for (int ni = 0; ni < NI; ++ni)
+        bias4[ni] = *reinterpret_cast<const float4*>(p.bias + n0 + wn * WN + ni * 16 + 4 * q4);
+    }
+  };
+  // Staged through `stage`: each wave's region holds 64 rows; the wave writes the
+  // results of four 16-row blocks, reads them back 16 bytes per lane along the rows
+  // and stores whole row segments, then does the same for the other four blocks.
+  // Only the wave's own region is touched between the two barriers around the
+  // epilogue, so the halves need no barrier of their own.
+  auto epilogue = [&](int stage, int64_t m0, int n0) __attribute__((always_inline)) {
+    uint8_t* ep = lds + stage * STAGE_BYTES + wave * (HALF_ROWS * OUT_ROWB);
+    const int jc = lane % OUT_CH;
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+#pragma unroll
+      for (int mh = 0; mh < MI / 2; ++mh) {
+        const int mi = h * (MI / 2) + mh;
+        const int r = mh * 16 + rl;
+#pragma unroll
+        for (int ni = 0; ni < NI; ++ni) {
+          float y[4] = {acc[mi][ni][0], acc[mi][ni][1], acc[mi][ni][2], acc[mi][ni][3]};
+          if constexpr (EP == Epi::kBiasClamp) {
+            const float bb[4] = {bias4[ni].x, bias4[ni].y, bias4[ni].z, bias4[ni].w};
+#pragma unroll
+            for (int j = 0; j < 4; ++j) y[j] = fminf(fmaxf(y[j] + bb[j], p.lo), p.hi);
+          }
+          const int col = ni * 16 + 4 * q4;
+          uint2 o;
+          o.x = pack_bf16x2(y[0], y[1]);
+          o.y = pack_bf16x2(y[2], y[3]);
+          const int ch = (col >> 3) ^ (r % OUT_CH);
+          *reinterpret_cast<uint2*>(ep + r * OUT_ROWB + ch * 16 + ((col >> 2) & 1) * 8) = o;
+        }
+      }
+      __builtin_amdgcn_s_waitcnt(waitcnt_imm(63, 0));
+      // Each store takes its data from a read of the region, so the region is read
+      // in full before the next half overwrites it.
+      uint16_t* crow = p.c + (m0 + wm * WM + h * HALF_ROWS + lane / OUT_CH) * p.ldc + n0 + wn * WN + jc * 8;
+#pragma unroll 4
+      for (int i = 0; i < HALF_ROWS / RPI; ++i) {
+        const int r = i * RPI + lane / OUT_CH;
+        const uint4 v = *reinterpret_cast<const uint4*>(ep + r * OUT_ROWB + ((jc ^ (r % OUT_CH)) << 4));
+        store_nt16(crow + (int64_t)i * RPI * p.ldc, v);
+      }
+    }
+  };
+
+  // ---- prologue: the first tile's steps 0 and 1 in flight, step 0 landed ---------
+#pragma unroll
+  for (int s = 0; s < kStages; ++s) {
+#pragma unroll
+    for (int d = 0; d < LD_PER_STEP; ++d) dma1(refill_src(s), s, d);
+  }
+  __builtin_amdgcn_s_waitcnt(waitcnt_imm(LD_PER_STEP, 15));
+  __syncthreads();
+  read_frags(0, 0, 0);
+  __builtin_amdgcn_s_waitcnt(waitcnt_imm(63, 0));
+  __builtin_amdgcn_sched_barrier(0);
+
+  int stage = 0;
+  zero_acc();
+  while (true) {
+    for (int kt = 0; kt + 1 < KT; ++kt) {
+      kstep(kt, stage, stage ^ 1, false, false);
+      stage ^= 1;
+    }
+    load_bias(cur_n0);
+    // The tile's last step: its wait and barrier also cover the next tile's step 0
+    // (the refill of step KT - 2); afterwards nobody reads `stage`.
+    kstep(KT - 1, stage, stage ^ 1, false, true);
+    epilogue(stage, cur_m0, cur_n0);
+    if (!has_next) break;
+    // Every wave is done with the staging region (its reads were waited for above):
+    // the next tile's step 1 goes there.  A plain barrier: the stores just issued
+    // need not be complete.
+    __builtin_amdgcn_s_barrier();
+    __builtin_amdgcn_sched_barrier(0);
+    ti += x_blocks;
+    cur_m0 = nxt_m0;
+    cur_n0 = nxt_n0;
+    cur_a = nxt_a;
+    cur_a2 = nxt_a2;
+    cur_b = nxt_b;
+    cur_b2 = nxt_b2;
+    has_next = ti + x_blocks < x_count;
+    tile_at(has_next ? ti + x_blocks : ti, nxt_m0, nxt_n0, nxt_a, nxt_a2, nxt_b, nxt_b2);
+#pragma unroll
+    for (int d = 0; d < LD_PER_STEP; ++d) dma1(StepSrc{kBK, false, true}, stage, d);
+    stage ^= 1;  // the next tile's step 0
+    read_frags(stage, 0, 0);
+    zero_acc();
+    __builtin_amdgcn_s_waitcnt(waitcnt_imm(63, 0));
+    __builtin_amdgcn_sched_barrier(0);
+  }
+}
+
+}  // namespace cdx

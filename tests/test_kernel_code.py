@@ -7,7 +7,10 @@ inside the K loop, which costs 20-30 % of the kernel's time without changing any
 result; a range check on permutation entries once did exactly that to the MoE
 gate/up pass.  This test compiles cdx_gemm.hip to assembly (hipcc, no GPU needed)
 and checks that the K loop of every engine instantiation is free of both and holds
-the expected MFMA count per iteration (two K32 sub-steps of 8 x 8 blocks).
+the expected MFMA count per iteration (two K32 sub-steps of 8 x 8 blocks).  The
+persistent form (gemm_persist_kernel) nests its K loop inside the loop over tiles; its
+K-loop block (the one issuing a whole step's 128 MFMAs and 16 DMAs) gets the same
+checks, and the kernel as a whole must not touch scratch memory.
 """
 
 from __future__ import annotations
@@ -54,3 +57,26 @@ def test_gemm_k_loops_have_no_register_shuffles(gemm_asm):
             f"{name}: VGPR/AGPR shuffles inside the K loop"
         assert "scratch_" not in loop and "buffer_store" not in loop, f"{name}: spills inside the K loop"
     assert seen >= 10
+
+
+def _blocks(body: str):
+    parts = re.split(r"^(\.LBB\d+_\d+):", body, flags=re.M)
+    yield "entry", parts[0]
+    for i in range(1, len(parts), 2):
+        yield parts[i], parts[i + 1]
+
+
+def test_persistent_gemm_k_loops_have_no_register_shuffles(gemm_asm):
+    seen = 0
+    for name in re.findall(r"^(_ZN3cdx19gemm_persist_kernel\S+):", gemm_asm, re.M):
+        start = gemm_asm.index(name + ":")
+        body = gemm_asm[start:gemm_asm.index(".Lfunc_end", start)]
+        assert "scratch_" not in body, f"{name}: scratch memory in use"
+        k_loops = [txt for _, txt in _blocks(body)
+                   if txt.count("v_mfma_f32_16x16x32_bf16") == 128 and txt.count(" lds") == 16]
+        assert k_loops, f"{name}: no K-loop block with 128 MFMAs and 16 DMAs"
+        for loop in k_loops:
+            assert "v_accvgpr_read" not in loop and "v_accvgpr_write" not in loop, \
+                f"{name}: VGPR/AGPR shuffles inside the K loop"
+        seen += 1
+    assert seen >= 3
