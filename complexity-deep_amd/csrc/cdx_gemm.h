@@ -181,6 +181,74 @@ __device__ __forceinline__ void buf_dma16(__amdgpu_buffer_rsrc_t r, uint32_t vof
                                            0, 0);
 }
 
+// ---- QK-norm + RoPE epilogue pieces (shared by the engine's two kernel forms) ----
+// For one 16-row block of one head: lane l holds row l & 15 and, in x[nb][0..3], the
+// head's columns 16 nb + 4 (l >> 4) + (0..3) (lanes l, l ^ 16, l ^ 32, l ^ 48 together
+// hold the row's HD = 16 BPH values).  In place: RMSNorm over the head (weights wf,
+// all ones and a unit scale without QK norm), then RoPE on each pair (c, c + HD/2),
+// whose elements sit in blocks nb and nb + BPH/2 of the same lane:
+//   y[c] = x[c] cos - x[c + HD/2] sin,  y[c + HD/2] = x[c + HD/2] cos + x[c] sin,
+// with cs[nb] the (cos, sin) pairs of this lane's first-half columns for its row.
+template <int BPH>
+__device__ __forceinline__ void qk_norm_rope(float (&x)[BPH][4], const float (&wf)[BPH][4],
+                                             const float4 (&cs)[BPH / 2][2], bool norm, float eps) {
+  // Four independent partial sums keep the chain short; the partners' sums come in
+  // through a swizzle (l ^ 16) and v_permlane32_swap (l ^ 32), neither touching LDS.
+  float s4[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int nb = 0; nb < BPH; ++nb)
+#pragma unroll
+    for (int v = 0; v < 4; ++v) s4[v] = __builtin_fmaf(x[nb][v], x[nb][v], s4[v]);
+  float ss = (s4[0] + s4[1]) + (s4[2] + s4[3]);
+  // ds_swizzle bit mode, and-mask 0x1f, xor-mask 0x10: lane l reads lane l ^ 16.
+  ss += __int_as_float(__builtin_amdgcn_ds_swizzle(__float_as_int(ss), 0x401F));
+  const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(ss), __float_as_uint(ss), false, false);
+  ss = __uint_as_float(sw[0]) + __uint_as_float(sw[1]);
+  // ss / HD + eps >= eps > 0 is a normal number: the plain hardware reciprocal square
+  // root needs no denormal scaling.  Without QK norm the weights are 1 and the scale
+  // is 1: both products are then exact, and there is no branch between the norm and
+  // the rotation (a branch there made the compiler pass the values through AGPRs).
+  const float rs = norm ? __builtin_amdgcn_rsqf(ss / (float)(16 * BPH) + eps) : 1.f;
+#pragma unroll
+  for (int nb = 0; nb < BPH; ++nb)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) x[nb][j] = wf[nb][j] * (x[nb][j] * rs);
+#pragma unroll
+  for (int nb = 0; nb < BPH / 2; ++nb) {
+    const float4 t01 = cs[nb][0], t23 = cs[nb][1];
+    const float cv[4] = {t01.x, t01.z, t23.x, t23.z};
+    const float sv[4] = {t01.y, t01.w, t23.y, t23.w};
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const float a = x[nb][j], bq = x[nb + BPH / 2][j];
+      x[nb][j] = a * cv[j] - bq * sv[j];
+      x[nb + BPH / 2][j] = bq * cv[j] + a * sv[j];
+    }
+  }
+}
+
+// V^T quad transpose: lanes 4j + t (same l >> 4) hold tokens 4j + t of dims
+// 4 (l >> 4) + (0..3) in x0..x3; afterwards lane 4j + t holds dim 4 (l >> 4) + t of
+// tokens 4j + (0..3), as two packed bf16 pairs, after two exchanges (lane t ^ 1, then
+// t ^ 2) over the quad.
+__device__ __forceinline__ uint2 vt_quad_transpose(float x0, float x1, float x2, float x3, int lane) {
+  const int t = lane & 3;
+  const bool odd = t & 1, upper = t & 2;
+  const uint32_t p0 = pack_bf16x2(x0, x1), p1 = pack_bf16x2(x2, x3);
+  // first exchange: even lanes give dims 1, 3 and keep 0, 2; odd lanes the reverse.
+  const uint32_t give = __builtin_amdgcn_perm(p1, p0, odd ? 0x05040100u : 0x07060302u);
+  const uint32_t got = (uint32_t)__builtin_amdgcn_mov_dpp((int)give, 0xB1, 0xF, 0xF, true);
+  const uint32_t a0 = __builtin_amdgcn_perm(got, p0, odd ? 0x03020504u : 0x05040100u);
+  const uint32_t a1 = __builtin_amdgcn_perm(got, p1, odd ? 0x03020706u : 0x07060100u);
+  // second exchange: lanes t < 2 give their second pair, t >= 2 their first.
+  const uint32_t give2 = upper ? a0 : a1;
+  const uint32_t got2 = (uint32_t)__builtin_amdgcn_mov_dpp((int)give2, 0x4E, 0xF, 0xF, true);
+  uint2 w;
+  w.x = upper ? got2 : a0;  // tokens 4j, 4j + 1
+  w.y = upper ? a1 : got2;  // tokens 4j + 2, 4j + 3
+  return w;
+}
+
 template <class Cfg, ALoad AL, Epi EP, int HD = 0>
 __global__ __launch_bounds__(kGemmThreads, Cfg::MINB) void gemm_nt_kernel(const GemmParams p) {
   constexpr int kBN = Cfg::BN, kBK = Cfg::BK, kStages = Cfg::STAGES;
@@ -690,21 +758,9 @@ __global__ __launch_bounds__(kGemmThreads, Cfg::MINB) void gemm_nt_kernel(const 
             // 4j + (0..3), as two packed bf16 pairs, in two exchanges (lane t ^ 1,
             // then t ^ 2) over the quad.
             const int t = lane & 3, j = (lane >> 2) & 3;
-            const bool odd = t & 1, upper = t & 2;
 #pragma unroll
             for (int nb = 0; nb < BPH; ++nb) {
-              const uint32_t p0 = pack_bf16x2(x[nb][0], x[nb][1]), p1 = pack_bf16x2(x[nb][2], x[nb][3]);
-              // first exchange: even lanes give dims 1, 3 and keep 0, 2; odd lanes the reverse.
-              const uint32_t give = __builtin_amdgcn_perm(p1, p0, odd ? 0x05040100u : 0x07060302u);
-              const uint32_t got = (uint32_t)__builtin_amdgcn_mov_dpp((int)give, 0xB1, 0xF, 0xF, true);
-              const uint32_t a0 = __builtin_amdgcn_perm(got, p0, odd ? 0x03020504u : 0x05040100u);
-              const uint32_t a1 = __builtin_amdgcn_perm(got, p1, odd ? 0x03020706u : 0x07060100u);
-              // second exchange: lanes t < 2 give their second pair, t >= 2 their first.
-              const uint32_t give2 = upper ? a0 : a1;
-              const uint32_t got2 = (uint32_t)__builtin_amdgcn_mov_dpp((int)give2, 0x4E, 0xF, 0xF, true);
-              uint2 w;
-              w.x = upper ? got2 : a0;  // tokens 4j, 4j + 1
-              w.y = upper ? a1 : got2;  // tokens 4j + 2, 4j + 3
+              const uint2 w = vt_quad_transpose(x[nb][0], x[nb][1], x[nb][2], x[nb][3], lane);
               // Tokens r .. r + 3 (r = 16 mi + 4 j) sit at V^T positions
               // 16 mi + 4 sigma(j) .. + 3; rows are 256 bytes with 16-byte chunk k
               // at position k ^ (row % 16).
@@ -737,48 +793,11 @@ __global__ __launch_bounds__(kGemmThreads, Cfg::MINB) void gemm_nt_kernel(const 
           continue;
         }
         fetch_cs(mi, cs_cur);
-        {
-          // RMSNorm over the head: this lane's quarter plus its three partners' (lanes
-          // l ^ 16 through a swizzle, l ^ 32 through v_permlane32_swap, neither of which
-          // touches LDS memory); four independent partial sums keep the chain short.
-          float s4[4] = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-          for (int nb = 0; nb < BPH; ++nb)
-#pragma unroll
-            for (int v = 0; v < 4; ++v) s4[v] = __builtin_fmaf(x[nb][v], x[nb][v], s4[v]);
-          float ss = (s4[0] + s4[1]) + (s4[2] + s4[3]);
-          // ds_swizzle bit mode, and-mask 0x1f, xor-mask 0x10: lane l reads lane l ^ 16.
-          ss += __int_as_float(__builtin_amdgcn_ds_swizzle(__float_as_int(ss), 0x401F));
-          const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(ss), __float_as_uint(ss), false, false);
-          ss = __uint_as_float(sw[0]) + __uint_as_float(sw[1]);
-          // ss / HD + eps >= eps > 0 is a normal number: the plain hardware reciprocal
-          // square root needs no denormal scaling.
-          const float rs = norm ? __builtin_amdgcn_rsqf(ss / (float)HD + q.eps) : 1.f;
-#pragma unroll
-          for (int nb = 0; nb < BPH; ++nb)
-#pragma unroll
-            for (int j = 0; j < 4; ++j) x[nb][j] = wf[nb][j] * (x[nb][j] * rs);
-        }
+        qk_norm_rope<BPH>(x, wf, cs_cur, norm, q.eps);
         if (gm >= m_end) continue;
-        // RoPE on each pair (c, c + HALF), c < HALF, sharing the angle of index c:
-        //   y[c] = x[c] cos - x[c + HALF] sin,  y[c + HALF] = x[c + HALF] cos + x[c] sin.
 #pragma unroll
-        for (int nb = 0; nb < BPH / 2; ++nb) {
-          const int c = nb * 16 + 4 * q4;  // first-half column, c % 4 == 0
-          const float4 t01 = cs_cur[nb][0], t23 = cs_cur[nb][1];
-          const float cv[4] = {t01.x, t01.z, t23.x, t23.z};
-          const float sv[4] = {t01.y, t01.w, t23.y, t23.w};
-          float lo[4], up[4];
-#pragma unroll
-          for (int j = 0; j < 4; ++j) {
-            const float a = x[nb][j];
-            const float bq = x[nb + BPH / 2][j];
-            lo[j] = a * cv[j] - bq * sv[j];
-            up[j] = bq * cv[j] + a * sv[j];
-          }
-          stage4(r, hb * HD + c, lo[0], lo[1], lo[2], lo[3]);
-          stage4(r, hb * HD + c + HALF, up[0], up[1], up[2], up[3]);
-        }
+        for (int nb = 0; nb < BPH; ++nb)
+          stage4(r, hb * HD + nb * 16 + 4 * q4, x[nb][0], x[nb][1], x[nb][2], x[nb][3]);
       }
     }
   } else if constexpr (EP == Epi::kSwiGLU) {

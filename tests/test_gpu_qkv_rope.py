@@ -152,3 +152,49 @@ def test_attention_fused_matches_unfused_path(cdx, monkeypatch, H, nq, nkv, with
     d = (fused.float() - unfused.float()).abs().max() / unfused.float().abs().max()
     print("max rel fused vs unfused", float(d), flush=True)
     assert float(d) < 3e-2
+
+
+@pytest.mark.parametrize("B,S,H,nq,nkv,mu_mode,pos0", [
+    (8, 2048, 2048, 16, 8, "full", 0),       # the 1B layer: D = 128, 64 x 16 tiles
+    (16, 1024, 768, 12, 4, "broadcast", 0),  # D = 64: 64 x 5 tiles
+    (64, 512, 512, 16, 4, None, 0),          # D = 32, no mu (K = H = 512): 128 x 3 tiles
+    (32, 520, 1024, 8, 4, "full", 3),        # D = 128, S % 16 != 0: waves span two sequences
+])
+def test_qkv_rope_many_tiles(cdx, oracle, B, S, H, nq, nkv, mu_mode, pos0):
+    """More tiles than CUs at each head dim, V stored plain and transposed (the
+    transposed V must equal the plain V moved into that layout bit for bit), and
+    sequences that do not split into whole 128-row waves: rows of two sequences in
+    one wave take the per-row token division and the element-wise V^T stores."""
+    from complexity_deep.attention import mu_qkv_rope, to_vt_layout
+    from complexity_deep.rotary import RotaryEmbedding
+    D = H // nq
+    print(f"qkv_rope many tiles B={B} S={S} H={H} heads={nq}/{nkv} D={D} mu={mu_mode} pos0={pos0}", flush=True)
+    g = torch.Generator().manual_seed(B * S + H)
+    x = torch.randn(B, S, H, generator=g).to(bf16)
+    if mu_mode == "full":
+        mu = torch.randn(B, S, H, generator=g).clamp(-2, 2).to(bf16)
+    elif mu_mode == "broadcast":
+        mu = (torch.randn(1, 1, H, generator=g) * 0.5).to(bf16).expand(B, S, H)
+    else:
+        mu = None
+    ws = [(torch.randn(d, H, generator=g) * 0.02).to(bf16) for d in (nq * D, nkv * D, nkv * D) * 2]
+    qn = (1 + 0.1 * torch.randn(D, generator=g)).to(bf16)
+    kn = (1 + 0.1 * torch.randn(D, generator=g)).to(bf16)
+    rot = RotaryEmbedding(D).cuda()
+    table = rot.cos_sin_table(pos0 + S, torch.device("cuda"))
+    wx = torch.cat(ws[:3], 0)
+    w_pack = (torch.cat([wx, torch.cat(ws[3:], 0)], 1) if mu is not None else wx).contiguous().cuda()
+    xd = x.cuda()
+    mud = None if mu is None else (mu.cuda() if mu_mode == "full" else mu[:1, :1].cuda().expand(B, S, H))
+    args = (xd, mud, w_pack, H, nq, nkv, D, qn.cuda(), kn.cuda(), 1e-6, table, pos0)
+    q, k, v = mu_qkv_rope(*args)
+    q2, k2, vt = mu_qkv_rope(*args, v_transposed=True)
+    torch.cuda.synchronize()
+    assert torch.equal(q, q2) and torch.equal(k, k2)
+    assert torch.equal(vt, to_vt_layout(v)), "transposed V differs from the plain V"
+    for b in (0, B - 1):
+        rq, rk, rv = _reference(oracle, x[b:b + 1], None if mu is None else mu[b:b + 1], ws, nq, nkv, D, qn, kn,
+                                rot.inv_freq.cpu(), pos0)
+        assert_close_bf16(q[b:b + 1], rq, f"q[{b}]")
+        assert_close_bf16(k[b:b + 1], rk, f"k[{b}]")
+        assert_close_bf16(v[b:b + 1], rv, f"v[{b}]")
