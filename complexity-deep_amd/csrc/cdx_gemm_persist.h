@@ -1,5 +1,7 @@
-// Persistent form of the MFMA tile engine (cdx_gemm.h) for whole tiles of a dense or
-// concat A operand (M and N multiples of the tile, no expert segments).
+// Persistent form of the MFMA tile engine (cdx_gemm.h): whole tiles of a dense or
+// concat A operand (M and N multiples of the tile) with the store or bias-clamp
+// epilogue, and the MoE gate/up pass (rows gathered through the routing permutation,
+// per-expert M tiles, SwiGLU epilogue).
 //
 // gemm_nt_kernel runs one tile per block, so every tile pays a block launch, its setup
 // and a prologue that waits for its first K step to arrive from L2 or HBM.  Here a grid
@@ -8,9 +10,10 @@
 // a tile's second-to-last K step is the next tile's first step, so that step lands
 // while the tile finishes and writes its results.  The epilogue stages the results
 // through the other LDS stage in two halves of 64 rows per wave (16 KB per wave, one
-// stage in all); the next tile's second step is issued when it is done.  The first K
-// step of a tile starts its accumulators from zero (the MFMA's C operand is the
-// constant 0), so nothing clears them between tiles.
+// stage in all; the SwiGLU output, half as wide, fits at once); the next tile's second
+// step is issued when it is done.  For gathered rows the next tile's per-lane source
+// offsets are computed from the permutation when the current tile starts.  The
+// accumulators are cleared between tiles.
 //
 // K loop, fragment reads, LDS layout, DMA placement and the staged-store layout are
 // those of gemm_nt_kernel.
@@ -22,8 +25,10 @@ namespace cdx {
 
 template <class Cfg, ALoad AL, Epi EP>
 __global__ __launch_bounds__(kGemmThreads, 1) void gemm_persist_kernel(const GemmParams p) {
-  static_assert(AL == ALoad::kDense || AL == ALoad::kConcat, "persistent tiles: dense or concat A only");
-  static_assert(EP == Epi::kStore || EP == Epi::kBiasClamp, "persistent tiles: store or bias-clamp epilogue");
+  constexpr bool kGathered = AL == ALoad::kGather;
+  static_assert(((AL == ALoad::kDense || AL == ALoad::kConcat) && (EP == Epi::kStore || EP == Epi::kBiasClamp)) ||
+                    (kGathered && EP == Epi::kSwiGLU),
+                "persistent tiles: dense/concat A with store or bias-clamp, or gathered A with SwiGLU");
   static_assert(Cfg::STAGES == 2 && Cfg::MINB == 1 && Cfg::BN == 256, "persistent tiles: 256 x 256, two stages");
   constexpr int kBN = Cfg::BN, kBK = Cfg::BK, kStages = 2;
   constexpr int ROW_BYTES = kBK * 2;
@@ -41,10 +46,12 @@ __global__ __launch_bounds__(kGemmThreads, 1) void gemm_persist_kernel(const Gem
   constexpr int NFRAG = MI + NI;
   constexpr int DMA_EVERY = Cfg::DMA_EVERY, DMA_OFF = Cfg::DMA_OFF, RD_EVERY = Cfg::READ_EVERY;
   // Epilogue staging: per wave and half, 64 rows of WN bf16 (256 bytes), 16-byte
-  // chunk c of row r at position c ^ (r % 16).
-  constexpr int OUT_ROWB = WN * 2, OUT_CH = OUT_ROWB / 16, HALF_ROWS = WM / 2, RPI = 64 / OUT_CH;
+  // chunk c of row r at position c ^ (r % 16); SwiGLU: all WM rows of WN / 2 columns.
+  constexpr int OUT_ROWB = (EP == Epi::kSwiGLU ? WN / 2 : WN) * 2, OUT_CH = OUT_ROWB / 16;
+  constexpr int HALF_ROWS = WM / 2, RPI = 64 / OUT_CH;
   static_assert(NSUB == 2, "one K step is two K32 sub-steps");
   static_assert(4 * HALF_ROWS * OUT_ROWB <= STAGE_BYTES, "a staged half must fit one stage");
+  static_assert(EP != Epi::kSwiGLU || 4 * WM * OUT_ROWB <= STAGE_BYTES, "the SwiGLU tile must fit one stage");
 
   __shared__ __attribute__((aligned(1024))) uint8_t lds[kStages * STAGE_BYTES];
 
@@ -54,9 +61,23 @@ __global__ __launch_bounds__(kGemmThreads, 1) void gemm_persist_kernel(const Gem
   const int wm = wave >> 1, wn = wave & 1;
 
   // ---- this block's tiles ------------------------------------------------------
+  // Segment offsets are read clamped to [0, M], and a segment that ends before it
+  // starts is empty (as in gemm_nt_kernel): offsets that are not a valid plan give
+  // wrong rows but no access outside the operands.  Grouped tiles: each M tile lies in
+  // one expert's segment; the launch bound p.mt_count caps the real count.
+  auto seg_off = [&](int x) __attribute__((always_inline)) {
+    const int v = p.offsets[x];
+    return v < 0 ? 0 : (v > (int)p.M ? (int)p.M : v);
+  };
+  int mt_real = p.mt_count;
+  if constexpr (kGathered) {
+    mt_real = 0;
+    for (int x = 0; x < p.E; ++x) mt_real += max(0, (seg_off(x + 1) - seg_off(x) + kBM - 1) / kBM);
+    mt_real = min(mt_real, p.mt_count);
+  }
   // XCD x (blocks b with b % 8 == x) owns logical tiles [x_first, x_first + x_count);
   // its k-th block takes tiles x_first + k, x_first + k + x_blocks, ...
-  const int tiles = p.mt_count * p.nt_count;
+  const int tiles = mt_real * p.nt_count;
   const int xcd = blockIdx.x % kNumXcd, kx = blockIdx.x / kNumXcd;
   const int tq = tiles / kNumXcd, tr = tiles % kNumXcd;
   const int x_first = xcd < tr ? xcd * (tq + 1) : tr * (tq + 1) + (xcd - tr) * tq;
@@ -68,18 +89,41 @@ __global__ __launch_bounds__(kGemmThreads, 1) void gemm_persist_kernel(const Gem
   // rows of the tile; concat: also the mu and mu-weight sources, k_split columns before
   // their first column, so that both K halves take the scalar offset 2 k0).  Separate
   // scalars: a struct selected through a reference ends up in scratch memory.
-  auto tile_at = [&](int i, int64_t& m0, int& n0, uintptr_t& a, uintptr_t& a2, uintptr_t& b, uintptr_t& b2)
-                     __attribute__((always_inline)) {
+  // Grouped: m0 / m_end are the tile's rows in the sorted order, its expert's B rows
+  // start at b + e * b_estride, and A is the whole gather source.
+  auto tile_at = [&](int i, int64_t& m0, int64_t& m_end, int& n0, uintptr_t& a, uintptr_t& a2, uintptr_t& b,
+                     uintptr_t& b2) __attribute__((always_inline)) {
     const int L = x_first + i;
     const int per_group = kGroupM * p.nt_count;
     const int group = L / per_group;
     const int first_m = group * kGroupM;
-    const int gsz = min(p.mt_count - first_m, kGroupM);
+    const int gsz = min(mt_real - first_m, kGroupM);
     const int in_group = L - group * per_group;
-    m0 = (int64_t)__builtin_amdgcn_readfirstlane(first_m + in_group % gsz) * kBM;
+    const int mt = __builtin_amdgcn_readfirstlane(first_m + in_group % gsz);
     n0 = __builtin_amdgcn_readfirstlane(in_group / gsz) * kBN;
-    a = (uintptr_t)(p.a + m0 * p.lda);
-    b = (uintptr_t)(p.b + (int64_t)n0 * p.ldb);
+    int e = 0;
+    if constexpr (kGathered) {
+      int before = 0;
+      m0 = 0;
+      m_end = 0;
+      for (int x = 0; x < p.E; ++x) {
+        const int s0 = seg_off(x), s1 = seg_off(x + 1);
+        const int ntile = max(0, (s1 - s0 + kBM - 1) / kBM);
+        if (mt < before + ntile) {
+          e = x;
+          m0 = s0 + (int64_t)(mt - before) * kBM;
+          m_end = s1;
+          break;
+        }
+        before += ntile;
+      }
+      a = (uintptr_t)p.a;
+    } else {
+      m0 = (int64_t)mt * kBM;
+      m_end = m0 + kBM;
+      a = (uintptr_t)(p.a + m0 * p.lda);
+    }
+    b = (uintptr_t)(p.b + (int64_t)e * p.b_estride + (int64_t)n0 * p.ldb);
     if constexpr (AL == ALoad::kConcat) {
       a2 = (uintptr_t)(p.a2 + m0 * p.lda2) - (uintptr_t)p.k_split * 2;
       b2 = (uintptr_t)(p.b2 + (int64_t)n0 * p.ldb) - (uintptr_t)p.k_split * 2;
@@ -90,6 +134,7 @@ __global__ __launch_bounds__(kGemmThreads, 1) void gemm_persist_kernel(const Gem
   };
 
   // ---- per-lane DMA offsets (the same for every whole tile) ----------------------
+  // Gathered rows: per tile, from the permutation (see gather_offsets below).
   const int dr = lane / CPR;
   uint32_t a_off[LD_A], a2_off[LD_A], b_off[LD_B];
 #pragma unroll
@@ -111,12 +156,32 @@ __global__ __launch_bounds__(kGemmThreads, 1) void gemm_persist_kernel(const Gem
   const int KT = p.K / kBK;  // the host guarantees KT >= 2
   const __amdgpu_buffer_rsrc_t rs_none = make_rsrc(p.b, 0u);
   int ti = kx;  // index of the current tile in the XCD's range
-  int64_t cur_m0, nxt_m0;
+  int64_t cur_m0, nxt_m0, cur_m_end, nxt_m_end;
   int cur_n0, nxt_n0;
   uintptr_t cur_a, cur_a2, cur_b, cur_b2, nxt_a, nxt_a2, nxt_b, nxt_b2;
-  tile_at(ti, cur_m0, cur_n0, cur_a, cur_a2, cur_b, cur_b2);
+  tile_at(ti, cur_m0, cur_m_end, cur_n0, cur_a, cur_a2, cur_b, cur_b2);
   bool has_next = ti + x_blocks < x_count;
-  tile_at(has_next ? ti + x_blocks : ti, nxt_m0, nxt_n0, nxt_a, nxt_a2, nxt_b, nxt_b2);
+  tile_at(has_next ? ti + x_blocks : ti, nxt_m0, nxt_m_end, nxt_n0, nxt_a, nxt_a2, nxt_b, nxt_b2);
+  // Gathered rows: the source row of each lane's DMA rows, through the permutation;
+  // rows past the segment repeat its last row (loaded, never stored), and an entry
+  // outside [0, M) is clamped into it (a corrupt permutation reads wrong rows but stays
+  // inside the operand; the host bounds M * lda * 2 to 4 GB).
+  uint32_t cur_goff[kGathered ? LD_A : 1], nxt_goff[kGathered ? LD_A : 1];
+  auto gather_offsets = [&](int64_t m0, int64_t m_end, uint32_t (&off)[kGathered ? LD_A : 1])
+                            __attribute__((always_inline)) {
+    if constexpr (kGathered) {
+#pragma unroll
+      for (int j = 0; j < LD_A; ++j) {
+        const int r = wave * (kBM / 4) + j * ROWS_PER_DMA + dr;
+        const int dchunk = (lane % CPR) ^ ((r / RPL) % CPR);
+        const int64_t gm = max(min(m0 + r, m_end - 1), (int64_t)0);
+        const uint32_t src = min((uint32_t)p.perm[gm], (uint32_t)(p.M - 1));
+        off[j] = (src * (uint32_t)p.lda + (uint32_t)dchunk * 8u) * 2u;
+      }
+    }
+  };
+  gather_offsets(cur_m0, cur_m_end, cur_goff);
+  if (has_next) gather_offsets(nxt_m0, nxt_m_end, nxt_goff);
 
   // Where a DMA reads: k0, the current or the next tile, and whether there is one.
   struct StepSrc {
@@ -131,17 +196,14 @@ __global__ __launch_bounds__(kGemmThreads, 1) void gemm_persist_kernel(const Gem
     if (d < LD_A) {
       const uintptr_t first_src = st.next ? nxt_a : cur_a, second_src = st.next ? nxt_a2 : cur_a2;
       const __amdgpu_buffer_rsrc_t r = make_rsrc((const void*)(second ? second_src : first_src));
-      buf_dma16(st.live ? r : rs_none, second ? a2_off[d] : a_off[d], (uint32_t)k0 * 2, dst + a_dma_off + d * 1024);
+      uint32_t off = second ? a2_off[d] : a_off[d];
+      if constexpr (kGathered) off = st.next ? nxt_goff[d] : cur_goff[d];
+      buf_dma16(st.live ? r : rs_none, off, (uint32_t)k0 * 2, dst + a_dma_off + d * 1024);
     } else {
       const uintptr_t first_src = st.next ? nxt_b : cur_b, second_src = st.next ? nxt_b2 : cur_b2;
       const __amdgpu_buffer_rsrc_t r = make_rsrc((const void*)(second ? second_src : first_src));
       buf_dma16(st.live ? r : rs_none, b_off[d - LD_A], (uint32_t)k0 * 2, dst + b_dma_off + (d - LD_A) * 1024);
     }
-  };
-  // Refill of step g of the current tile's stream: its own steps, then the next
-  // tile's first step (step KT), fetching nothing after the block's last tile.
-  auto refill_src = [&](int g) __attribute__((always_inline)) {
-    return g < KT ? StepSrc{g * kBK, false, true} : StepSrc{0, true, has_next};
   };
 
   // ---- fragments ---------------------------------------------------------------
@@ -179,32 +241,33 @@ __global__ __launch_bounds__(kGemmThreads, 1) void gemm_persist_kernel(const Gem
         asm volatile("" : "+a"(acc[mi][ni]));
       }
   };
-  auto mfma1 = [&](int set, int i, bool first) __attribute__((always_inline)) {
+  auto mfma1 = [&](int set, int i) __attribute__((always_inline)) {
     const int mi = i / NI, ni = i % NI;
-    (void)first;
     acc[mi][ni] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(fb[set][ni], fa[set][mi], acc[mi][ni], 0, 0, 0);
   };
 
   // ---- K step --------------------------------------------------------------------
-  // Sub-step 0: its MFMAs (from zero accumulators on a tile's first step) with the
-  // fragment reads of sub-step 1 behind them.  Sub-step 1: wait for the next step's
-  // DMA and the barrier, then its MFMAs with the refill of the freed stage (step
-  // kt + 2) and the fragment reads of step kt + 1, both left out on the tile's last
-  // step (its stage then stages the results).
-  auto kstep = [&](int kt, int stage, int next_stage, bool first, bool last) __attribute__((always_inline)) {
+  // Sub-step 0: its MFMAs with the fragment reads of sub-step 1 behind them.
+  // Sub-step 1: wait for the next step's DMA and the barrier, then its MFMAs with the
+  // refill of the freed stage and the fragment reads of step kt + 1.
+  // The refill is step kt + 2 of the tile, or the next tile's first step (none after
+  // the block's last tile); the tile's last step neither refills nor reads the next
+  // step's fragments (its stage then stages the results).
+  auto kstep = [&](int kt, int stage, int next_stage, bool last) __attribute__((always_inline)) {
 #pragma unroll
     for (int i = 0; i < MI * NI; ++i) {
-      mfma1(0, i, first);
+      mfma1(0, i);
       if (i % RD_EVERY == 0 && i / RD_EVERY < NFRAG) read1(stage, 1, 1, i / RD_EVERY);
       __builtin_amdgcn_sched_barrier(0);
     }
-    const StepSrc st = refill_src(kt + kStages);
+    const int g = kt + kStages;
+    const StepSrc st = g < KT ? StepSrc{g * kBK, false, true} : StepSrc{0, true, has_next};
     __builtin_amdgcn_s_waitcnt(waitcnt_imm(0, 0));
     __syncthreads();
     __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
     for (int i = 0; i < MI * NI; ++i) {
-      mfma1(1, i, false);
+      mfma1(1, i);
       if (!last && i % DMA_EVERY == DMA_OFF && i / DMA_EVERY < LD_PER_STEP) dma1(st, stage, i / DMA_EVERY);
       if (!last && i % RD_EVERY == 0 && i / RD_EVERY < NFRAG) read1(next_stage, 0, 0, i / RD_EVERY);
       __builtin_amdgcn_sched_barrier(0);
@@ -233,9 +296,44 @@ __global__ __launch_bounds__(kGemmThreads, 1) void gemm_persist_kernel(const Gem
   // and stores whole row segments, then does the same for the other four blocks.
   // Only the wave's own region is touched between the two barriers around the
   // epilogue, so the halves need no barrier of their own.
-  auto epilogue = [&](int stage, int64_t m0, int n0) __attribute__((always_inline)) {
-    uint8_t* ep = lds + stage * STAGE_BYTES + wave * (HALF_ROWS * OUT_ROWB);
+  // SwiGLU: packed B rows come in groups of 64, 32 gate rows then the matching 32 up
+  // rows (blocks 4 g, 4 g + 1 gate, 4 g + 2, 4 g + 3 up); the wave's output columns
+  // are 32 g + 16 (ni % 4) + 4 q4, all WM rows staged at once; rows at or past the
+  // segment's end are not stored.
+  auto epilogue = [&](int stage, int64_t m0, int64_t m_end, int n0) __attribute__((always_inline)) {
     const int jc = lane % OUT_CH;
+    if constexpr (EP == Epi::kSwiGLU) {
+      uint8_t* ep = lds + stage * STAGE_BYTES + wave * (WM * OUT_ROWB);
+#pragma unroll
+      for (int mi = 0; mi < MI; ++mi) {
+        const int r = mi * 16 + rl;
+#pragma unroll
+        for (int ni = 0; ni < NI; ni += 4)
+#pragma unroll
+          for (int h = 0; h < 2; ++h) {
+            float a4[4];
+#pragma unroll
+            for (int j = 0; j < 4; ++j) a4[j] = silu_f32(acc[mi][ni + h][j]) * acc[mi][ni + h + 2][j];
+            const int col = (ni >> 2) * 32 + 16 * h + 4 * q4;
+            uint2 o;
+            o.x = pack_bf16x2(a4[0], a4[1]);
+            o.y = pack_bf16x2(a4[2], a4[3]);
+            const int ch = (col >> 3) ^ (r % OUT_CH);
+            *reinterpret_cast<uint2*>(ep + r * OUT_ROWB + ch * 16 + ((col >> 2) & 1) * 8) = o;
+          }
+      }
+      __builtin_amdgcn_s_waitcnt(waitcnt_imm(63, 0));
+      const int n = (n0 + wn * WN) / 2 + jc * 8;
+#pragma unroll 4
+      for (int i = 0; i < WM / RPI; ++i) {
+        const int r = i * RPI + lane / OUT_CH;
+        const int64_t gm = m0 + wm * WM + r;
+        const uint4 v = *reinterpret_cast<const uint4*>(ep + r * OUT_ROWB + ((jc ^ (r % OUT_CH)) << 4));
+        if (gm < m_end && 2 * n < p.N) store_nt16(p.c + gm * p.ldc + n, v);
+      }
+      return;
+    }
+    uint8_t* ep = lds + stage * STAGE_BYTES + wave * (HALF_ROWS * OUT_ROWB);
 #pragma unroll
     for (int h = 0; h < 2; ++h) {
 #pragma unroll
@@ -275,7 +373,7 @@ __global__ __launch_bounds__(kGemmThreads, 1) void gemm_persist_kernel(const Gem
 #pragma unroll
   for (int s = 0; s < kStages; ++s) {
 #pragma unroll
-    for (int d = 0; d < LD_PER_STEP; ++d) dma1(refill_src(s), s, d);
+    for (int d = 0; d < LD_PER_STEP; ++d) dma1(StepSrc{s * kBK, false, true}, s, d);
   }
   __builtin_amdgcn_s_waitcnt(waitcnt_imm(LD_PER_STEP, 15));
   __syncthreads();
@@ -287,14 +385,14 @@ __global__ __launch_bounds__(kGemmThreads, 1) void gemm_persist_kernel(const Gem
   zero_acc();
   while (true) {
     for (int kt = 0; kt + 1 < KT; ++kt) {
-      kstep(kt, stage, stage ^ 1, false, false);
+      kstep(kt, stage, stage ^ 1, false);
       stage ^= 1;
     }
     load_bias(cur_n0);
-    // The tile's last step: its wait and barrier also cover the next tile's step 0
-    // (the refill of step KT - 2); afterwards nobody reads `stage`.
-    kstep(KT - 1, stage, stage ^ 1, false, true);
-    epilogue(stage, cur_m0, cur_n0);
+    // The tile's last step: its wait and barrier also cover the next tile's step 0;
+    // afterwards nobody reads `stage`.
+    kstep(KT - 1, stage, stage ^ 1, true);
+    epilogue(stage, cur_m0, cur_m_end, cur_n0);
     if (!has_next) break;
     // Every wave is done with the staging region (its reads were waited for above):
     // the next tile's step 1 goes there.  A plain barrier: the stores just issued
@@ -303,13 +401,19 @@ __global__ __launch_bounds__(kGemmThreads, 1) void gemm_persist_kernel(const Gem
     __builtin_amdgcn_sched_barrier(0);
     ti += x_blocks;
     cur_m0 = nxt_m0;
+    cur_m_end = nxt_m_end;
     cur_n0 = nxt_n0;
     cur_a = nxt_a;
     cur_a2 = nxt_a2;
     cur_b = nxt_b;
     cur_b2 = nxt_b2;
     has_next = ti + x_blocks < x_count;
-    tile_at(has_next ? ti + x_blocks : ti, nxt_m0, nxt_n0, nxt_a, nxt_a2, nxt_b, nxt_b2);
+    tile_at(has_next ? ti + x_blocks : ti, nxt_m0, nxt_m_end, nxt_n0, nxt_a, nxt_a2, nxt_b, nxt_b2);
+    if constexpr (kGathered) {
+#pragma unroll
+      for (int j = 0; j < LD_A; ++j) cur_goff[j] = nxt_goff[j];
+      if (has_next) gather_offsets(nxt_m0, nxt_m_end, nxt_goff);
+    }
 #pragma unroll
     for (int d = 0; d < LD_PER_STEP; ++d) dma1(StepSrc{kBK, false, true}, stage, d);
     stage ^= 1;  // the next tile's step 0

@@ -128,6 +128,31 @@ def test_moe_down_tiles_across_experts(cdx, oracle, T, H, I, E, shared, empty):
     assert_close_bf16(out, ref, "spanning tiles")
 
 
+@pytest.mark.parametrize("T,H,I,E,shared,empty", [(32768, 512, 8192, 16, True, (3, 9, 15)),
+                                                  (20000, 256, 4096, 4, False, (0,)),
+                                                  (9000, 128, 2048, 2, True, ())])
+def test_moe_gate_up_many_tiles(cdx, oracle, T, H, I, E, shared, empty):
+    """Gate/up passes with several per-expert tiles per CU and whole column tiles
+    (2 P a multiple of 256, P the padded expert width), which run on the persistent form
+    of the tile engine: ragged segments, empty experts (the last one in the first case),
+    K = H of 4 steps and of 2 (the minimum, where a tile's first refill is already the
+    next tile's first step).  Checked against the oracle, and a second call must give
+    the same bits."""
+    print(f"moe gate/up many tiles T={T} H={H} I={I} E={E} shared={shared} empty={empty}", flush=True)
+    g = torch.Generator().manual_seed(T + H)
+    live = torch.tensor([e for e in range(E) if e not in empty])
+    V = 4000
+    tmap = live[torch.randint(0, len(live), (V,), generator=g)]
+    m = _module(cdx, H, I, E, V, shared, T, tmap)
+    ids = torch.randint(0, V, (T,), generator=g)
+    x = torch.randn(T, H, generator=g).to(bf16).cuda()
+    out = _run(m, x.view(1, T, H), ids.view(1, T).cuda())
+    again = _run(m, x.view(1, T, H), ids.view(1, T).cuda())
+    assert torch.equal(out, again)
+    ref = _oracle(oracle, m, x.view(1, T, H), ids.view(1, T))
+    assert_close_bf16(out, ref, "gate/up many tiles")
+
+
 def test_moe_average_all_experts(cdx, oracle):
     print("moe token_ids=None", flush=True)
     m = _module(cdx, 256, 512, 4, 100, True, 9)
