@@ -220,9 +220,10 @@ __device__ __forceinline__ void qk_norm_rope(float (&x)[BPH][4], const float (&w
     const float sv[4] = {t01.y, t01.w, t23.y, t23.w};
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
+      // Explicit FMAs: the contraction is then the same wherever this is inlined.
       const float a = x[nb][j], bq = x[nb + BPH / 2][j];
-      x[nb][j] = a * cv[j] - bq * sv[j];
-      x[nb + BPH / 2][j] = bq * cv[j] + a * sv[j];
+      x[nb][j] = __builtin_fmaf(a, cv[j], -(bq * sv[j]));
+      x[nb + BPH / 2][j] = __builtin_fmaf(bq, cv[j], a * sv[j]);
     }
   }
 }

@@ -25,19 +25,23 @@ int launch(GemmParams p, hipStream_t s, const char* name) {
   // The kernel's K loop runs at least once and whole steps only.
   if (p.K < Cfg::BK || p.K % Cfg::BK != 0)
     return fail(CDX_EUNSUPPORTED, "%s: K=%d must be a positive multiple of %d", name, p.K, Cfg::BK);
-  // Whole tiles of a plain (unsegmented) product, and the gathered SwiGLU pass with
-  // whole N tiles, run on the persistent form when they have more tiles than CUs: one
-  // block per CU (a multiple of 8, so that every XCD's share of the tiles has blocks)
-  // walking its XCD's tiles.  (For the gathered pass nb is the launch bound on the
-  // per-expert tiles; the kernel counts the real ones.)
+  // Whole tiles of a plain (unsegmented) product, the gathered SwiGLU pass with whole
+  // N tiles, and mu-QKV with the QK-norm + RoPE epilogue (head dim 128, V transposed,
+  // whole M tiles, sequences a multiple of 128 tokens) run on the persistent form when
+  // they have more tiles than CUs: one block per CU (a multiple of 8, so that every
+  // XCD's share of the tiles has blocks) walking its XCD's tiles.  (For the gathered
+  // pass nb is the launch bound on the per-expert tiles; the kernel counts the real
+  // ones.)
   constexpr bool kDenseTiles =
       (AL == ALoad::kDense || AL == ALoad::kConcat) && (EP == Epi::kStore || EP == Epi::kBiasClamp);
   constexpr bool kGatherTiles = AL == ALoad::kGather && EP == Epi::kSwiGLU;
-  if constexpr ((kDenseTiles || kGatherTiles) && Cfg::BN == 256) {
+  constexpr bool kRopeTiles = AL == ALoad::kConcat && EP == Epi::kQKRope && HD == 128;
+  if constexpr ((kDenseTiles || kGatherTiles || kRopeTiles) && Cfg::BN == 256) {
     const int64_t grid = (device_cu_count() + kNumXcd - 1) / kNumXcd * kNumXcd;
-    const bool whole = kGatherTiles ? p.offsets != nullptr : (p.offsets == nullptr && p.M % kBM == 0);
+    bool whole = kGatherTiles ? p.offsets != nullptr : (p.offsets == nullptr && p.M % kBM == 0);
+    if (kRopeTiles) whole = whole && p.qk.vt_ld > 0 && p.qk.S % (kBM / 2) == 0;
     if (whole && p.N % Cfg::BN == 0 && p.K >= 2 * Cfg::BK && nb > grid) {
-      gemm_persist_kernel<Cfg, AL, EP><<<dim3((unsigned)grid), dim3(kGemmThreads), 0, s>>>(p);
+      gemm_persist_kernel<Cfg, AL, EP, HD><<<dim3((unsigned)grid), dim3(kGemmThreads), 0, s>>>(p);
       return check_launch(name);
     }
   }

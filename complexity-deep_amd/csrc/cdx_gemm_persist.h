@@ -1,7 +1,8 @@
 // Persistent form of the MFMA tile engine (cdx_gemm.h): whole tiles of a dense or
 // concat A operand (M and N multiples of the tile) with the store or bias-clamp
-// epilogue, and the MoE gate/up pass (rows gathered through the routing permutation,
-// per-expert M tiles, SwiGLU epilogue).
+// epilogue, mu-QKV with the QK-norm + RoPE epilogue (head dim 128, V transposed), and
+// the MoE gate/up pass (rows gathered through the routing permutation, per-expert M
+// tiles, SwiGLU epilogue).
 //
 // gemm_nt_kernel runs one tile per block, so every tile pays a block launch, its setup
 // and a prologue that waits for its first K step to arrive from L2 or HBM.  Here a grid
@@ -23,12 +24,13 @@
 
 namespace cdx {
 
-template <class Cfg, ALoad AL, Epi EP>
+template <class Cfg, ALoad AL, Epi EP, int HD = 0>
 __global__ __launch_bounds__(kGemmThreads, 1) void gemm_persist_kernel(const GemmParams p) {
   constexpr bool kGathered = AL == ALoad::kGather;
   static_assert(((AL == ALoad::kDense || AL == ALoad::kConcat) && (EP == Epi::kStore || EP == Epi::kBiasClamp)) ||
-                    (kGathered && EP == Epi::kSwiGLU),
-                "persistent tiles: dense/concat A with store or bias-clamp, or gathered A with SwiGLU");
+                    (kGathered && EP == Epi::kSwiGLU) || (AL == ALoad::kConcat && EP == Epi::kQKRope && HD == 128),
+                "persistent tiles: dense/concat A with store or bias-clamp, gathered A with SwiGLU, or mu-QKV "
+                "with the QK-norm + RoPE epilogue at head dim 128");
   static_assert(Cfg::STAGES == 2 && Cfg::MINB == 1 && Cfg::BN == 256, "persistent tiles: 256 x 256, two stages");
   constexpr int kBN = Cfg::BN, kBK = Cfg::BK, kStages = 2;
   constexpr int ROW_BYTES = kBK * 2;
@@ -296,12 +298,135 @@ __global__ __launch_bounds__(kGemmThreads, 1) void gemm_persist_kernel(const Gem
   // and stores whole row segments, then does the same for the other four blocks.
   // Only the wave's own region is touched between the two barriers around the
   // epilogue, so the halves need no barrier of their own.
+  // QK-norm + RoPE (head dim 128, V transposed, S a multiple of WM): the wave's
+  // WN = HD columns are one head and its WM rows one run of tokens of one sequence.
+  // q and k heads are normalised and rotated block by block from the accumulators
+  // (qk_norm_rope) and staged like the plain store; a V head is staged transposed,
+  // per half as HD rows d of its 64 tokens (128 bytes, 16-byte chunk k of row d at
+  // position k ^ (d % 8)) in vt_col order, and stored as V^T row segments.  The lane
+  // index is passed through an empty asm first, so that nothing derived from it here
+  // is computed once and held through the K loop.
+  auto epilogue_rope = [&](int stage, int64_t m0, int n0) __attribute__((always_inline)) {
+    // (The lambda exists in every instance of the kernel; kHD keeps it well formed.)
+    constexpr int kHD = EP == Epi::kQKRope ? HD : 32, BPH = kHD / 16;
+    const QKRopeParams& q = p.qk;
+    int lo = lane;
+    asm volatile("" : "+v"(lo));
+    const int eq4 = lo >> 4, erl = lo & 15;
+    const int c0 = n0 + wn * WN;
+    const int qd = q.nq * kHD, kvd = q.nkv * kHD;
+    const int kind = c0 < qd ? 0 : (c0 < qd + kvd ? 1 : 2);  // q, k, v
+    const int head = kind == 0 ? c0 / kHD : (kind == 1 ? (c0 - qd) / kHD : (c0 - qd - kvd) / kHD);
+    const int64_t row0 = m0 + wm * WM;
+    const int64_t tb = row0 / q.S;
+    const int64_t ts0 = row0 - tb * q.S;
+    uint8_t* ep = lds + stage * STAGE_BYTES + wave * (HALF_ROWS * OUT_ROWB);
+    if (kind == 2) {
+      const int t = lo & 3, j = (lo >> 2) & 3;
+      const int sj = j == 1 ? 2 : (j == 2 ? 1 : j);
+      const int k = lo & 7;
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+#pragma unroll
+        for (int mh = 0; mh < MI / 2; ++mh) {
+          const int mi = h * (MI / 2) + mh;
+#pragma unroll
+          for (int nb = 0; nb < BPH; ++nb) {
+            const uint2 w = vt_quad_transpose(acc[mi][nb][0], acc[mi][nb][1], acc[mi][nb][2], acc[mi][nb][3], lo);
+            const int row = nb * 16 + 4 * eq4 + t;
+            const int chunk = 2 * mh + (sj >> 1);
+            *reinterpret_cast<uint2*>(ep + row * 128 + ((chunk ^ (row & 7)) << 4) + (sj & 1) * 8) = w;
+          }
+        }
+        __builtin_amdgcn_s_waitcnt(waitcnt_imm(63, 0));
+        uint16_t* vrow = q.v_out + ((tb * q.nkv + head) * kHD + (lo >> 3)) * q.vt_ld + ts0 + h * HALF_ROWS + k * 8;
+#pragma unroll 4
+        for (int i = 0; i < kHD / 8; ++i) {
+          const int row = i * 8 + (lo >> 3);
+          const uint4 v = *reinterpret_cast<const uint4*>(ep + row * 128 + ((k ^ (row & 7)) << 4));
+          store_nt16(vrow + (int64_t)i * 8 * q.vt_ld, v);
+        }
+      }
+      return;
+    }
+    // Norm weights of this lane's columns, fp32; all ones without QK norm (no branch
+    // between the norm and the rotation).
+    const uint16_t* nw = kind == 0 ? q.q_norm_w : q.k_norm_w;
+    const bool norm = nw != nullptr;
+    // Two bf16 ones, made opaque here: as a known constant the pair was set up once
+    // before the tile loop and spilled.
+    uint32_t one2 = 0x3F803F80u;
+    asm volatile("" : "+v"(one2));
+    uint2 wpk[BPH];
+#pragma unroll
+    for (int nb = 0; nb < BPH; ++nb) wpk[nb] = make_uint2(one2, one2);
+    if (norm) {
+#pragma unroll
+      for (int nb = 0; nb < BPH; ++nb) wpk[nb] = *reinterpret_cast<const uint2*>(nw + nb * 16 + 4 * eq4);
+    }
+    float wf[BPH][4];
+#pragma unroll
+    for (int nb = 0; nb < BPH; ++nb) {
+      wf[nb][0] = __uint_as_float(wpk[nb].x << 16);
+      wf[nb][1] = __uint_as_float(wpk[nb].x & 0xffff0000u);
+      wf[nb][2] = __uint_as_float(wpk[nb].y << 16);
+      wf[nb][3] = __uint_as_float(wpk[nb].y & 0xffff0000u);
+    }
+    const int jc = lo % OUT_CH;
+    uint16_t* obase = kind == 0 ? q.q_out : q.k_out;
+    const int nheads = kind == 0 ? q.nq : q.nkv;
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+#pragma unroll
+      for (int mh = 0; mh < MI / 2; ++mh) {
+        __builtin_amdgcn_sched_barrier(0);  // one block of accumulators live at a time
+        const int mi = h * (MI / 2) + mh;
+        const int r = mh * 16 + erl;
+        float x[BPH][4];
+#pragma unroll
+        for (int nb = 0; nb < BPH; ++nb)
+#pragma unroll
+          for (int v = 0; v < 4; ++v) x[nb][v] = acc[mi][nb][v];
+        // (cos, sin) of this lane's first-half columns at the row's position.
+        const float2* csp = reinterpret_cast<const float2*>(q.cos_sin) + (q.pos0 + ts0 + mi * 16 + erl) * (kHD / 2);
+        float4 cs[BPH / 2][2];
+#pragma unroll
+        for (int nb = 0; nb < BPH / 2; ++nb) {
+          const int c = nb * 16 + 4 * eq4;
+          cs[nb][0] = *reinterpret_cast<const float4*>(csp + c);
+          cs[nb][1] = *reinterpret_cast<const float4*>(csp + c + 2);
+        }
+        qk_norm_rope<BPH>(x, wf, cs, norm, q.eps);
+#pragma unroll
+        for (int nb = 0; nb < BPH; ++nb) {
+          const int col = nb * 16 + 4 * eq4;
+          uint2 o;
+          o.x = pack_bf16x2(x[nb][0], x[nb][1]);
+          o.y = pack_bf16x2(x[nb][2], x[nb][3]);
+          const int ch = (col >> 3) ^ (r % OUT_CH);
+          *reinterpret_cast<uint2*>(ep + r * OUT_ROWB + ch * 16 + ((col >> 2) & 1) * 8) = o;
+        }
+      }
+      __builtin_amdgcn_s_waitcnt(waitcnt_imm(63, 0));
+      uint16_t* orow = obase + ((tb * nheads + head) * q.S + ts0 + h * HALF_ROWS + lo / OUT_CH) * kHD + jc * 8;
+#pragma unroll 4
+      for (int i = 0; i < HALF_ROWS / RPI; ++i) {
+        const int r = i * RPI + lo / OUT_CH;
+        const uint4 v = *reinterpret_cast<const uint4*>(ep + r * OUT_ROWB + ((jc ^ (r % OUT_CH)) << 4));
+        store_nt16(orow + (int64_t)i * RPI * kHD, v);
+      }
+    }
+  };
   // SwiGLU: packed B rows come in groups of 64, 32 gate rows then the matching 32 up
   // rows (blocks 4 g, 4 g + 1 gate, 4 g + 2, 4 g + 3 up); the wave's output columns
   // are 32 g + 16 (ni % 4) + 4 q4, all WM rows staged at once; rows at or past the
   // segment's end are not stored.
   auto epilogue = [&](int stage, int64_t m0, int64_t m_end, int n0) __attribute__((always_inline)) {
     const int jc = lane % OUT_CH;
+    if constexpr (EP == Epi::kQKRope) {
+      epilogue_rope(stage, m0, n0);
+      return;
+    }
     if constexpr (EP == Epi::kSwiGLU) {
       uint8_t* ep = lds + stage * STAGE_BYTES + wave * (WM * OUT_ROWB);
 #pragma unroll
@@ -414,8 +539,12 @@ __global__ __launch_bounds__(kGemmThreads, 1) void gemm_persist_kernel(const Gem
       for (int j = 0; j < LD_A; ++j) cur_goff[j] = nxt_goff[j];
       if (has_next) gather_offsets(nxt_m0, nxt_m_end, nxt_goff);
     }
+    // An opaque K position: with kBK known, the compiler reused the prologue's A-offset
+    // selects for these DMAs and kept them (spilled) through the whole tile loop.
+    int k1 = kBK;
+    asm volatile("" : "+s"(k1));
 #pragma unroll
-    for (int d = 0; d < LD_PER_STEP; ++d) dma1(StepSrc{kBK, false, true}, stage, d);
+    for (int d = 0; d < LD_PER_STEP; ++d) dma1(StepSrc{k1, false, true}, stage, d);
     stage ^= 1;  // the next tile's step 0
     read_frags(stage, 0, 0);
     zero_acc();

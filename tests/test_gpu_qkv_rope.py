@@ -154,21 +154,27 @@ def test_attention_fused_matches_unfused_path(cdx, monkeypatch, H, nq, nkv, with
     assert float(d) < 3e-2
 
 
-@pytest.mark.parametrize("B,S,H,nq,nkv,mu_mode,pos0", [
-    (8, 2048, 2048, 16, 8, "full", 0),       # the 1B layer: D = 128, 64 x 16 tiles
-    (16, 1024, 768, 12, 4, "broadcast", 0),  # D = 64: 64 x 5 tiles
-    (64, 512, 512, 16, 4, None, 0),          # D = 32, no mu (K = H = 512): 128 x 3 tiles
-    (32, 520, 1024, 8, 4, "full", 3),        # D = 128, S % 16 != 0: waves span two sequences
+@pytest.mark.parametrize("B,S,H,nq,nkv,mu_mode,pos0,qk_norm", [
+    (8, 2048, 2048, 16, 8, "full", 0, True),       # the 1B layer: D = 128, 64 x 16 tiles
+    (16, 1024, 768, 12, 4, "broadcast", 0, True),  # D = 64: 64 x 5 tiles
+    (64, 512, 512, 16, 4, None, 0, True),          # D = 32, no mu (K = H = 512): 128 x 3 tiles
+    (32, 520, 1024, 8, 4, "full", 3, True),        # D = 128, S % 16 != 0: waves span two sequences
+    (32, 384, 1024, 8, 2, "broadcast", 5, True),   # D = 128, 48 x 6 tiles, M tiles span sequences
+    (24, 512, 1024, 8, 4, "full", 0, False),       # D = 128 without QK norm, 48 x 8 tiles
 ])
-def test_qkv_rope_many_tiles(cdx, oracle, B, S, H, nq, nkv, mu_mode, pos0):
+def test_qkv_rope_many_tiles(cdx, oracle, B, S, H, nq, nkv, mu_mode, pos0, qk_norm):
     """More tiles than CUs at each head dim, V stored plain and transposed (the
-    transposed V must equal the plain V moved into that layout bit for bit), and
-    sequences that do not split into whole 128-row waves: rows of two sequences in
-    one wave take the per-row token division and the element-wise V^T stores."""
+    transposed V must equal the plain V moved into that layout bit for bit, and q and
+    k must not depend on V's layout), and sequences that do not split into whole
+    128-row waves: rows of two sequences in one wave take the per-row token division
+    and the element-wise V^T stores.  At head dim 128 with whole 128-token runs the
+    transposed-V call runs the persistent form of the kernel and the plain-V call the
+    one-tile-per-block form, so the equalities compare the two bit for bit."""
     from complexity_deep.attention import mu_qkv_rope, to_vt_layout
     from complexity_deep.rotary import RotaryEmbedding
     D = H // nq
-    print(f"qkv_rope many tiles B={B} S={S} H={H} heads={nq}/{nkv} D={D} mu={mu_mode} pos0={pos0}", flush=True)
+    print(f"qkv_rope many tiles B={B} S={S} H={H} heads={nq}/{nkv} D={D} mu={mu_mode} pos0={pos0} "
+          f"qk_norm={qk_norm}", flush=True)
     g = torch.Generator().manual_seed(B * S + H)
     x = torch.randn(B, S, H, generator=g).to(bf16)
     if mu_mode == "full":
@@ -180,13 +186,16 @@ def test_qkv_rope_many_tiles(cdx, oracle, B, S, H, nq, nkv, mu_mode, pos0):
     ws = [(torch.randn(d, H, generator=g) * 0.02).to(bf16) for d in (nq * D, nkv * D, nkv * D) * 2]
     qn = (1 + 0.1 * torch.randn(D, generator=g)).to(bf16)
     kn = (1 + 0.1 * torch.randn(D, generator=g)).to(bf16)
+    if not qk_norm:
+        qn = kn = None
     rot = RotaryEmbedding(D).cuda()
     table = rot.cos_sin_table(pos0 + S, torch.device("cuda"))
     wx = torch.cat(ws[:3], 0)
     w_pack = (torch.cat([wx, torch.cat(ws[3:], 0)], 1) if mu is not None else wx).contiguous().cuda()
     xd = x.cuda()
     mud = None if mu is None else (mu.cuda() if mu_mode == "full" else mu[:1, :1].cuda().expand(B, S, H))
-    args = (xd, mud, w_pack, H, nq, nkv, D, qn.cuda(), kn.cuda(), 1e-6, table, pos0)
+    args = (xd, mud, w_pack, H, nq, nkv, D, None if qn is None else qn.cuda(), None if kn is None else kn.cuda(),
+            1e-6, table, pos0)
     q, k, v = mu_qkv_rope(*args)
     q2, k2, vt = mu_qkv_rope(*args, v_transposed=True)
     torch.cuda.synchronize()
