@@ -47,8 +47,9 @@ __global__ __launch_bounds__(kGemmThreads, 1) void gemm_persist_kernel(const Gem
   constexpr int NSUB = kBK / 32;
   constexpr int NFRAG = MI + NI;
   constexpr int DMA_EVERY = Cfg::DMA_EVERY, DMA_OFF = Cfg::DMA_OFF, RD_EVERY = Cfg::READ_EVERY;
-  // Epilogue staging: per wave and half, 64 rows of WN bf16 (256 bytes), 16-byte
-  // chunk c of row r at position c ^ (r % 16); SwiGLU: all WM rows of WN / 2 columns.
+  // Epilogue staging: per wave and half, 64 rows of WN bf16 (256 bytes); SwiGLU: all
+  // WM rows of WN / 2 columns (128 bytes).  16-byte chunk c of row r sits at position
+  // c ^ (r % OUT_CH).
   constexpr int OUT_ROWB = (EP == Epi::kSwiGLU ? WN / 2 : WN) * 2, OUT_CH = OUT_ROWB / 16;
   constexpr int HALF_ROWS = WM / 2, RPI = 64 / OUT_CH;
   static_assert(NSUB == 2, "one K step is two K32 sub-steps");
@@ -183,7 +184,9 @@ __global__ __launch_bounds__(kGemmThreads, 1) void gemm_persist_kernel(const Gem
     }
   };
   gather_offsets(cur_m0, cur_m_end, cur_goff);
-  if (has_next) gather_offsets(nxt_m0, nxt_m_end, nxt_goff);
+  // Without a next tile the "next" tile is the current one again (its offsets are set
+  // but never read from: the DMA that would fetch it takes the empty descriptor).
+  gather_offsets(nxt_m0, nxt_m_end, nxt_goff);
 
   // Where a DMA reads: k0, the current or the next tile, and whether there is one.
   struct StepSrc {
