@@ -9,6 +9,7 @@ brute force) on the same bf16 inputs and weights:
   * no shared expert, Ie needing padding (176 -> 192), E=1, an expert with no
     tokens, single tokens, the token_ids=None average path, the dense SwiGLU;
   * shapes whose down pass runs M tiles that span experts (empty experts inside);
+  * gate/up passes with several tiles per CU (the persistent form), up to 64 experts;
   * the grouped-GEMM operator API.
 """
 
@@ -130,14 +131,16 @@ def test_moe_down_tiles_across_experts(cdx, oracle, T, H, I, E, shared, empty):
 
 @pytest.mark.parametrize("T,H,I,E,shared,empty", [(32768, 512, 8192, 16, True, (3, 9, 15)),
                                                   (20000, 256, 4096, 4, False, (0,)),
-                                                  (9000, 128, 2048, 2, True, ())])
+                                                  (9000, 128, 2048, 2, True, ()),
+                                                  (32768, 256, 16384, 64, True, (5, 6, 40, 63))])
 def test_moe_gate_up_many_tiles(cdx, oracle, T, H, I, E, shared, empty):
     """Gate/up passes with several per-expert tiles per CU and whole column tiles
     (2 P a multiple of 256, P the padded expert width), which run on the persistent form
-    of the tile engine: ragged segments, empty experts (the last one in the first case),
-    K = H of 4 steps and of 2 (the minimum, where a tile's first refill is already the
-    next tile's first step).  Checked against the oracle, and a second call must give
-    the same bits."""
+    of the tile engine: ragged segments, empty experts (the last one in the first and
+    last cases), K = H of 4 steps and of 2 (the minimum, where a tile's first refill is
+    already the next tile's first step), and 64 experts (the limit) of about 500 tokens
+    each, i.e. a partial M tile per expert.  Checked against the oracle, and a second
+    call must give the same bits."""
     print(f"moe gate/up many tiles T={T} H={H} I={I} E={E} shared={shared} empty={empty}", flush=True)
     g = torch.Generator().manual_seed(T + H)
     live = torch.tensor([e for e in range(E) if e not in empty])
