@@ -16,11 +16,20 @@
 namespace cdx {
 namespace {
 
+// Tiles of 256 x 128 for products too small to fill the chip with 256 x 256 tiles.
+using NarrowCfg = GemmCfg<128, 64, 2, 1, 2, 1, 1>;
+
 template <ALoad AL, Epi EP, class Cfg = DefaultCfg, int HD = 0>
 int launch(GemmParams p, hipStream_t s, const char* name) {
   p.nt_count = (p.N + Cfg::BN - 1) / Cfg::BN;
   const int64_t nb = (int64_t)p.mt_count * p.nt_count;
   if (nb == 0) return CDX_OK;
+  // At most half as many 256 x 256 tiles as CUs (launch bound): half-width tiles give
+  // twice the blocks, each with half the MFMA work per K step, still in one round.
+  // (A head of 128 columns does not fit a narrow tile's 64-column waves.)
+  if constexpr (Cfg::BN == 256 && (EP != Epi::kQKRope || HD <= 64)) {
+    if (2 * nb <= device_cu_count()) return launch<AL, EP, NarrowCfg, HD>(p, s, name);
+  }
   if (nb > INT32_MAX) return fail(CDX_EUNSUPPORTED, "%s: problem too large (%lld tiles)", name, (long long)nb);
   // The kernel's K loop runs at least once and whole steps only.
   if (p.K < Cfg::BK || p.K % Cfg::BK != 0)
