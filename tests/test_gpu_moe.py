@@ -10,6 +10,7 @@ brute force) on the same bf16 inputs and weights:
     tokens, single tokens, the token_ids=None average path, the dense SwiGLU;
   * shapes whose down pass runs M tiles that span experts (empty experts inside);
   * gate/up passes with several tiles per CU (the persistent form), up to 64 experts;
+  * a token's output independent of its batch (tile forms and layouts agree bit for bit);
   * the grouped-GEMM operator API.
 """
 
@@ -230,3 +231,27 @@ def test_dense_swiglu_and_average_path_residual(cdx):
         got = r.clone()
         m(x, residual=got)
     assert torch.equal(got, expect)
+
+
+def test_moe_rows_independent_of_batch_and_tile_form(cdx):
+    """A token's MoE output does not depend on the rest of the batch: the first 300
+    tokens alone (per-expert tiles of 256 x 128, one tile per block) and inside the
+    configuration-4 batch of 16384 (persistent gate/up tiles, segmented down tiles that
+    span experts) give the same bits, residual add included.  Both accumulate every
+    output element over K in the same order (the shared columns first, then the
+    expert's; a spanning tile's passes over other experts' columns add exact zeros)."""
+    from complexity_deep import synthetic as syn
+    print("moe rows independent of batch", flush=True)
+    T, H, I, E, small = 16384, 2048, 5632, 8, 300
+    m = _module(cdx, H, I, E, 32000, True, 7, syn.binpacked_map(32000, E))
+    ids = syn.zipf_token_ids(1, T, 32000, seed=3).cuda()
+    x = syn.normal_bf16((1, T, H), seed=4).cuda()
+    r = syn.normal_bf16((1, T, H), seed=5).cuda()
+    with torch.no_grad():
+        full = m(x, token_ids=ids)
+        part = m(x[:, :small].contiguous(), token_ids=ids[:, :small].contiguous())
+        assert torch.equal(part, full[:, :small])
+        rfull, rpart = r.clone(), r[:, :small].clone()
+        m(x, token_ids=ids, residual=rfull)
+        m(x[:, :small].contiguous(), token_ids=ids[:, :small].contiguous(), residual=rpart)
+    assert torch.equal(rpart, rfull[:, :small])
