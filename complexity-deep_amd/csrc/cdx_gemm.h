@@ -314,18 +314,24 @@ __global__ __launch_bounds__(kGemmThreads, Cfg::MINB) void gemm_nt_kernel(const 
   int64_t m0, m_end, m_lo;
   int e = 0;
   int e_lo = 0, n_exp = 1;  // kSegmented: first expert of the tile, experts it touches
+  // kSegmented: lane x holds segment start offsets[x] for x < E (E <= 64), read in one
+  // vector load instead of a chain of scalar ones; the tile's experts follow by ballots.
+  int seg_lane = 0;
   if constexpr (AL == ALoad::kSegmented) {
     // Rows outside [offsets[0], offsets[E]) belong to no expert and are not stored.
     m0 = (int64_t)mt * kBM;
-    m_lo = max(m0, (int64_t)seg_off(0));
-    m_end = min(min(p.M, m0 + kBM), (int64_t)seg_off(p.E));
+    seg_lane = lane < p.E ? seg_off(lane) : (int)p.M;
+    m_lo = max(m0, (int64_t)__builtin_amdgcn_readfirstlane(seg_lane));
+    m_end = min(min(p.M, m0 + kBM), (int64_t)__builtin_amdgcn_readfirstlane(seg_off(p.E)));
     if (m_lo >= m_end) return;
-    // Experts holding rows m_lo and m_end - 1 (segments are consecutive and sorted).
-    int e_hi = 0;
-    for (int x = 0; x < p.E; ++x) {
-      if (seg_off(x) <= m_lo && m_lo < seg_off(x + 1)) e_lo = x;
-      if (seg_off(x) <= m_end - 1 && m_end - 1 < seg_off(x + 1)) e_hi = x;
-    }
+    // Experts holding rows m_lo and m_end - 1: for consecutive sorted segments, the
+    // number of segments after the first that start at or before the row (a segment
+    // that is empty or out of order gives wrong rows, never an expert outside [0, E)).
+    // (Pinned to scalar registers: the B descriptor is built from e_lo.)
+    const bool mid = lane >= 1 && lane < p.E;
+    e_lo = __builtin_amdgcn_readfirstlane(__builtin_popcountll(__builtin_amdgcn_ballot_w64(mid && seg_lane <= m_lo)));
+    const int e_hi =
+        __builtin_amdgcn_readfirstlane(__builtin_popcountll(__builtin_amdgcn_ballot_w64(mid && seg_lane <= m_end - 1)));
     n_exp = max(1, e_hi - e_lo + 1);
   } else if (p.offsets != nullptr) {
     int before = 0;
@@ -394,7 +400,7 @@ __global__ __launch_bounds__(kGemmThreads, Cfg::MINB) void gemm_nt_kernel(const 
       int ex = -1;
       if (gm >= m_lo && gm < m_end) {
         ex = e_lo;
-        for (int x = e_lo + 1; x < e_lo + n_exp; ++x) ex += seg_off(x) <= gm ? 1 : 0;
+        for (int x = e_lo + 1; x < e_lo + n_exp; ++x) ex += __builtin_amdgcn_readlane(seg_lane, x) <= gm ? 1 : 0;
       }
       a_exp[j] = ex;
     }
