@@ -56,7 +56,10 @@ __global__ __launch_bounds__(kGemmThreads, 1) void gemm_persist_kernel(const Gem
   static_assert(4 * HALF_ROWS * OUT_ROWB <= STAGE_BYTES, "a staged half must fit one stage");
   static_assert(EP != Epi::kSwiGLU || 4 * WM * OUT_ROWB <= STAGE_BYTES, "the SwiGLU tile must fit one stage");
 
-  __shared__ __attribute__((aligned(1024))) uint8_t lds[kStages * STAGE_BYTES];
+  // Gathered tiles: after the stages, a table of 3 x 64 ints (segment starts, ends and
+  // the running count of M tiles, one entry per expert).
+  constexpr int SEG_TAB_BYTES = kGathered ? 3 * 64 * 4 : 0;
+  __shared__ __attribute__((aligned(1024))) uint8_t lds[kStages * STAGE_BYTES + SEG_TAB_BYTES];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -72,11 +75,30 @@ __global__ __launch_bounds__(kGemmThreads, 1) void gemm_persist_kernel(const Gem
     const int v = p.offsets[x];
     return v < 0 ? 0 : (v > (int)p.M ? (int)p.M : v);
   };
+  // Gathered: lane x < E holds segment x's start and end and the number of M tiles of
+  // segments 0..x (an inclusive scan over the lanes), from two vector loads per block;
+  // tile decodes then take ballots and lane reads instead of a loop of dependent loads
+  // (a load in that loop waited for every outstanding memory operation, the previous
+  // tile's stores included).  Wave 0 keeps a copy in LDS for the decodes at tile
+  // switches, so that the values are not held in registers through the K loop.
   int mt_real = p.mt_count;
+  int g_s0 = 0, g_s1 = 0, g_ci = 0;
+  int* seg_tab = reinterpret_cast<int*>(lds + kStages * STAGE_BYTES);
   if constexpr (kGathered) {
-    mt_real = 0;
-    for (int x = 0; x < p.E; ++x) mt_real += max(0, (seg_off(x + 1) - seg_off(x) + kBM - 1) / kBM);
-    mt_real = min(mt_real, p.mt_count);
+    g_s0 = lane < p.E ? seg_off(lane) : (int)p.M;
+    g_s1 = lane < p.E ? seg_off(lane + 1) : (int)p.M;
+    g_ci = lane < p.E ? max(0, (g_s1 - g_s0 + kBM - 1) / kBM) : 0;
+#pragma unroll
+    for (int d = 1; d < 64; d <<= 1) {
+      const int up = __shfl_up(g_ci, d);
+      g_ci += lane >= d ? up : 0;
+    }
+    mt_real = min(__builtin_amdgcn_readlane(g_ci, 63), p.mt_count);
+    if (wave == 0) {
+      seg_tab[lane] = g_s0;
+      seg_tab[64 + lane] = g_s1;
+      seg_tab[128 + lane] = g_ci;
+    }
   }
   // XCD x (blocks b with b % 8 == x) owns logical tiles [x_first, x_first + x_count);
   // its k-th block takes tiles x_first + k, x_first + k + x_blocks, ...
@@ -95,7 +117,7 @@ __global__ __launch_bounds__(kGemmThreads, 1) void gemm_persist_kernel(const Gem
   // Grouped: m0 / m_end are the tile's rows in the sorted order, its expert's B rows
   // start at b + e * b_estride, and A is the whole gather source.
   auto tile_at = [&](int i, int64_t& m0, int64_t& m_end, int& n0, uintptr_t& a, uintptr_t& a2, uintptr_t& b,
-                     uintptr_t& b2) __attribute__((always_inline)) {
+                     uintptr_t& b2, int s0v, int s1v, int civ) __attribute__((always_inline)) {
     const int L = x_first + i;
     const int per_group = kGroupM * p.nt_count;
     const int group = L / per_group;
@@ -106,20 +128,13 @@ __global__ __launch_bounds__(kGemmThreads, 1) void gemm_persist_kernel(const Gem
     n0 = __builtin_amdgcn_readfirstlane(in_group / gsz) * kBN;
     int e = 0;
     if constexpr (kGathered) {
-      int before = 0;
-      m0 = 0;
-      m_end = 0;
-      for (int x = 0; x < p.E; ++x) {
-        const int s0 = seg_off(x), s1 = seg_off(x + 1);
-        const int ntile = max(0, (s1 - s0 + kBM - 1) / kBM);
-        if (mt < before + ntile) {
-          e = x;
-          m0 = s0 + (int64_t)(mt - before) * kBM;
-          m_end = s1;
-          break;
-        }
-        before += ntile;
-      }
+      // The segment holding M tile mt: the first whose running tile count exceeds mt
+      // (mt < mt_real keeps it below E).
+      e = min((int)__builtin_popcountll(__builtin_amdgcn_ballot_w64(lane < p.E && civ <= mt)), p.E - 1);
+      e = __builtin_amdgcn_readfirstlane(e);
+      const int before = e > 0 ? __builtin_amdgcn_readlane(civ, e - 1) : 0;
+      m0 = __builtin_amdgcn_readlane(s0v, e) + (int64_t)(mt - before) * kBM;
+      m_end = __builtin_amdgcn_readlane(s1v, e);
       a = (uintptr_t)p.a;
     } else {
       m0 = (int64_t)mt * kBM;
@@ -162,9 +177,9 @@ __global__ __launch_bounds__(kGemmThreads, 1) void gemm_persist_kernel(const Gem
   int64_t cur_m0, nxt_m0, cur_m_end, nxt_m_end;
   int cur_n0, nxt_n0;
   uintptr_t cur_a, cur_a2, cur_b, cur_b2, nxt_a, nxt_a2, nxt_b, nxt_b2;
-  tile_at(ti, cur_m0, cur_m_end, cur_n0, cur_a, cur_a2, cur_b, cur_b2);
+  tile_at(ti, cur_m0, cur_m_end, cur_n0, cur_a, cur_a2, cur_b, cur_b2, g_s0, g_s1, g_ci);
   bool has_next = ti + x_blocks < x_count;
-  tile_at(has_next ? ti + x_blocks : ti, nxt_m0, nxt_m_end, nxt_n0, nxt_a, nxt_a2, nxt_b, nxt_b2);
+  tile_at(has_next ? ti + x_blocks : ti, nxt_m0, nxt_m_end, nxt_n0, nxt_a, nxt_a2, nxt_b, nxt_b2, g_s0, g_s1, g_ci);
   // Gathered rows: the source row of each lane's DMA rows, through the permutation;
   // rows past the segment repeat its last row (loaded, never stored), and an entry
   // outside [0, M) is clamped into it (a corrupt permutation reads wrong rows but stays
@@ -536,7 +551,13 @@ __global__ __launch_bounds__(kGemmThreads, 1) void gemm_persist_kernel(const Gem
     cur_b = nxt_b;
     cur_b2 = nxt_b2;
     has_next = ti + x_blocks < x_count;
-    tile_at(has_next ? ti + x_blocks : ti, nxt_m0, nxt_m_end, nxt_n0, nxt_a, nxt_a2, nxt_b, nxt_b2);
+    int t_s0 = 0, t_s1 = 0, t_ci = 0;
+    if constexpr (kGathered) {
+      t_s0 = seg_tab[lane];
+      t_s1 = seg_tab[64 + lane];
+      t_ci = seg_tab[128 + lane];
+    }
+    tile_at(has_next ? ti + x_blocks : ti, nxt_m0, nxt_m_end, nxt_n0, nxt_a, nxt_a2, nxt_b, nxt_b2, t_s0, t_s1, t_ci);
     if constexpr (kGathered) {
 #pragma unroll
       for (int j = 0; j < LD_A; ++j) cur_goff[j] = nxt_goff[j];
