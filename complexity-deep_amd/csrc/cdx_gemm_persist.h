@@ -7,7 +7,8 @@
 // gemm_nt_kernel runs one tile per block, so every tile pays a block launch, its setup
 // and a prologue that waits for its first K step to arrive from L2 or HBM.  Here a grid
 // of one block per CU walks the tiles of its XCD's range (the same logical order as
-// gemm_nt_kernel: contiguous per XCD, groups of kGroupM M tiles).  The refill issued by
+// gemm_nt_kernel: contiguous per XCD, groups of kGroupM M tiles; with the QK-norm + RoPE
+// epilogue, odd groups take their N tiles in reverse).  The refill issued by
 // a tile's second-to-last K step is the next tile's first step, so that step lands
 // while the tile finishes and writes its results.  The epilogue stages the results
 // through the other LDS stage in two halves of 64 rows per wave (16 KB per wave, one
@@ -125,7 +126,14 @@ __global__ __launch_bounds__(kGemmThreads, 1) void gemm_persist_kernel(const Gem
     const int gsz = min(mt_real - first_m, kGroupM);
     const int in_group = L - group * per_group;
     const int mt = __builtin_amdgcn_readfirstlane(first_m + in_group % gsz);
-    n0 = __builtin_amdgcn_readfirstlane(in_group / gsz) * kBN;
+    // QK-norm + RoPE: odd groups walk the N tiles backwards (a serpentine), so that a
+    // block's tiles i and i + 2 x_blocks sit at mirrored columns and every block gets
+    // a mix of q, k and v heads, whose epilogues differ in cost (at the 1B shape half
+    // the blocks otherwise ran two q and two k tiles).  Measured slower for the MoE
+    // gate/up pass, so the other epilogues keep the plain order.
+    const int nt = in_group / gsz;
+    const bool rev = EP == Epi::kQKRope && (group & 1);
+    n0 = __builtin_amdgcn_readfirstlane(rev ? p.nt_count - 1 - nt : nt) * kBN;
     int e = 0;
     if constexpr (kGathered) {
       // The segment holding M tile mt: the first whose running tile count exceeds mt
