@@ -272,7 +272,10 @@ __global__ __launch_bounds__(kGemmThreads, Cfg::MINB) void gemm_nt_kernel(const 
   static_assert(EP != Epi::kSwiGLU || (WN % 64) == 0, "SwiGLU needs gate/up pairs per wave");
   static_assert(LD_PER_STEP * (kStages - 1) <= 63, "vmcnt range");
 
-  __shared__ __attribute__((aligned(1024))) uint8_t lds[kStages * STAGE_BYTES];
+  // Scatter epilogues: after the stages, the output row (permutation entry) of each of
+  // the tile's kBM rows, loaded in the prologue.
+  constexpr bool kScatterRows = EP == Epi::kScatter || EP == Epi::kScatterAdd;
+  __shared__ __attribute__((aligned(1024))) uint8_t lds[kStages * STAGE_BYTES + (kScatterRows ? kBM * 4 : 0)];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -588,9 +591,21 @@ __global__ __launch_bounds__(kGemmThreads, Cfg::MINB) void gemm_nt_kernel(const 
     last_substep(kt, stage, next_stage, last);
   };
 
-  // Prologue: steps 0 .. kStages-1 in flight, step 0 landed.
+  // Prologue: steps 0 .. kStages-1 in flight, step 0 landed.  Scatter epilogues: thread
+  // r < kBM first loads row r's permutation entry, which lands with step 0 and goes to
+  // LDS, so that the epilogue's residual loads need no dependent global load.
+  // Entries are clamped into [0, M) (a corrupt permutation scrambles rows but stays in
+  // C); rows past the segment repeat its last row's (read, never stored).
+  int32_t* perm_lds = reinterpret_cast<int32_t*>(lds + kStages * STAGE_BYTES);
+  int32_t perm_pre = 0;
+  if constexpr (kScatterRows) {
+    if (tid < kBM) perm_pre = p.perm[m0 + tid < m_end ? m0 + tid : m_end - 1];
+  }
   for (int i = 0; i < kStages; ++i) issue(i, i);
   __builtin_amdgcn_s_waitcnt(waitcnt_imm(LD_PER_STEP * (kStages - 1), 15));
+  if constexpr (kScatterRows) {
+    if (tid < kBM) perm_lds[tid] = perm_pre < 0 ? 0 : (perm_pre >= (int32_t)p.M ? (int32_t)p.M - 1 : perm_pre);
+  }
   __syncthreads();
   read_frags(0, 0, 0);
   __builtin_amdgcn_s_waitcnt(waitcnt_imm(63, 0));
@@ -627,26 +642,19 @@ __global__ __launch_bounds__(kGemmThreads, Cfg::MINB) void gemm_nt_kernel(const 
   static_assert(4 * WM * OUT_ROWB <= kStages * STAGE_BYTES, "epilogue staging must fit the LDS");
   __syncthreads();  // every wave is done with the pipeline's LDS stages
   uint8_t* ep = lds + wave * (WM * OUT_ROWB);
-  // Scatter epilogues: the output row of every store-loop iteration (perm) and, for
-  // kScatterAdd, every residual piece this lane adds to are loaded up front, before
-  // the accumulators are staged, so that the two dependent load latencies (perm, then
-  // the residual row) run under the staging instead of after it (loads interleaved
-  // with the stores below would wait one by one: a store may alias a later row's
-  // load).
+  // Scatter epilogues: the output row of every store-loop iteration (from the LDS copy
+  // of the permutation) and, for kScatterAdd, every residual piece this lane adds to
+  // are loaded up front, before the accumulators are staged, so that the residual
+  // loads' latency runs under the staging instead of after it (loads interleaved with
+  // the stores below would wait one by one: a store may alias a later row's load).
   // Rows past the segment and columns past N read a clamped, valid piece (never
   // stored): guarded loads would become branches, each waiting for its load.
   constexpr int NIT = WM / RPI;  // store-loop iterations per lane
-  constexpr bool kScatterRows = EP == Epi::kScatter || EP == Epi::kScatterAdd;
   int32_t prow[kScatterRows ? NIT : 1];
   uint4 resid[EP == Epi::kScatterAdd ? NIT : 1];
   if constexpr (kScatterRows) {
 #pragma unroll
-    for (int i = 0; i < NIT; ++i) {
-      const int64_t gm = m0 + wm * WM + i * RPI + lane / OUT_CH;
-      // Clamped into [0, M): a corrupt permutation scrambles rows but stays in C.
-      const int32_t pr = p.perm[gm < m_end ? gm : m_end - 1];
-      prow[i] = pr < 0 ? 0 : (pr >= (int32_t)p.M ? (int32_t)p.M - 1 : pr);
-    }
+    for (int i = 0; i < NIT; ++i) prow[i] = perm_lds[wm * WM + i * RPI + lane / OUT_CH];
   }
   if constexpr (EP == Epi::kScatterAdd) {
     const int n = min(n0 + wn * WN + (lane % OUT_CH) * 8, p.N - 8);
