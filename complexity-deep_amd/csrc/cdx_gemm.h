@@ -743,7 +743,11 @@ __global__ __launch_bounds__(kGemmThreads, Cfg::MINB) void gemm_nt_kernel(const 
       // the top of the block so that the latency hides behind the norm arithmetic.
       // Every row's s lies in [0, S), so the reads stay inside the table even past
       // m_end.
-      float4 cs_cur[BPH / 2][2];
+      // Narrow tiles (the small products, whose blocks have no neighbours on their CU
+      // to hide a wait) read block mi + 1's pairs while block mi is computed; the wide
+      // tile has no registers to spare for them.
+      constexpr bool kCsAhead = kBN == 128;
+      float4 cs_cur[BPH / 2][2], cs_nxt[BPH / 2][2];
       auto fetch_cs = [&](int mi, float4 (&dst)[BPH / 2][2]) __attribute__((always_inline)) {
         int64_t b;
         uint32_t s;
@@ -756,6 +760,7 @@ __global__ __launch_bounds__(kGemmThreads, Cfg::MINB) void gemm_nt_kernel(const 
           dst[nb][1] = *reinterpret_cast<const float4*>(cs + c + 2);
         }
       };
+      if (kCsAhead && kind != 2) fetch_cs(0, cs_nxt);
 #pragma unroll
       for (int mi = 0; mi < MI; ++mi) {
         __builtin_amdgcn_sched_barrier(0);  // one block of accumulators live at a time
@@ -807,7 +812,16 @@ __global__ __launch_bounds__(kGemmThreads, Cfg::MINB) void gemm_nt_kernel(const 
             stage4(r, hb * HD + nb * 16 + 4 * q4, x[nb][0], x[nb][1], x[nb][2], x[nb][3]);
           continue;
         }
-        fetch_cs(mi, cs_cur);
+        if constexpr (kCsAhead) {
+#pragma unroll
+          for (int nb = 0; nb < BPH / 2; ++nb) {
+            cs_cur[nb][0] = cs_nxt[nb][0];
+            cs_cur[nb][1] = cs_nxt[nb][1];
+          }
+          if (mi + 1 < MI) fetch_cs(mi + 1, cs_nxt);
+        } else {
+          fetch_cs(mi, cs_cur);
+        }
         qk_norm_rope<BPH>(x, wf, cs_cur, norm, q.eps);
         if (gm >= m_end) continue;
 #pragma unroll

@@ -17,7 +17,9 @@ namespace cdx {
 namespace {
 
 // Tiles of 256 x 128 for products too small to fill the chip with 256 x 256 tiles.
-using NarrowCfg = GemmCfg<128, 64, 2, 1, 2, 1, 1>;
+// Their K steps are half as long, so three stages (144 KB) give each load two steps
+// to land; refills ride behind every fourth MFMA of the step.
+using NarrowCfg = GemmCfg<128, 64, 3, 1, 4, 1, 1>;
 
 template <ALoad AL, Epi EP, class Cfg = DefaultCfg, int HD = 0>
 int launch(GemmParams p, hipStream_t s, const char* name) {
