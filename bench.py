@@ -13,6 +13,8 @@ tokens per second with inputs already in HBM.
 The other workloads run one configuration each:
   "readme-forward"  configuration 1: the reference README's model (hidden 768, 18
                     layers, 12/4 heads, E=4 + shared), batch 4 x seq 512, seed 0
+  "readme-forward-graph"  the same forward replayed from a HIP graph recorded once
+                    (GraphedForward; at this size Python's launch rate paces eager)
   "moe-layer"       configuration 2: TokenRoutedMLP, 16384 x 768, E=4, Ie=512 + shared
   "qkv-norm"        configuration 3: add+RMSNorm then mu-QKV, 32768 x 2048, 16q/8kv x 128
   "route-stress"    configuration 5: routing plan + MoE layer, 65536 tokens, 90% skew
@@ -233,6 +235,24 @@ def workload_readme(args, dev):
     return step, ids.numel(), config, ("mu_qkv",), None
 
 
+def workload_readme_graph(args, dev):
+    import torch
+    cfg, model, ids_cpu = build_readme(dev)
+    model = model.to(dev, torch.bfloat16).eval()
+    ids = ids_cpu.to(dev)
+    graphed = model.capture_forward(*ids.shape)
+
+    def step():
+        return graphed(ids)
+
+    config = {"workload": "configuration 1 (as readme-forward), each forward replayed from a HIP graph "
+                          "recorded once (GraphedForward): the same kernels on the same buffers, issued from the "
+                          "device queue instead of by Python", "hidden": 768, "layers": 18,
+              "global_batch": 4, "seq_len": 512, "tokens_per_step": ids.numel(),
+              "note": "no per-launch events in a replay: no kernels table"}
+    return step, ids.numel(), config, (), None
+
+
 def workload_route_permute(args, dev):
     import torch
     from complexity_deep import synthetic as syn
@@ -363,11 +383,12 @@ def workload_route_stress(args, dev):
     return step, T, config, ("moe_swiglu", "route_plan"), None
 
 
-WORKLOADS = {"1b-forward": workload_1b, "readme-forward": workload_readme, "moe-layer": workload_moe,
+WORKLOADS = {"1b-forward": workload_1b, "readme-forward": workload_readme,
+             "readme-forward-graph": workload_readme_graph, "moe-layer": workload_moe,
              "qkv-norm": workload_qkv_norm, "route-stress": workload_route_stress,
              "route-permute": workload_route_permute, "rmsnorm-1b": workload_rmsnorm,
              "attention-1b": workload_attention}
-EXTRAS = ("readme-forward", "moe-layer", "qkv-norm", "route-stress", "route-permute", "rmsnorm-1b", "attention-1b")
+EXTRAS = ("readme-forward", "readme-forward-graph", "moe-layer", "qkv-norm", "route-stress", "route-permute", "rmsnorm-1b", "attention-1b")
 
 
 # ---------------------------------------------------------------------------

@@ -17,7 +17,7 @@ on the kernels in libcdx.so; the forward is inference-only (no backward).
 from .attention import ComplexityAttention, FusedMuQKVProjection, MuGuidedAttention, fused_mu_qkv_projection
 from .layer import MuGuidance, TransformerBlock
 from .mlp import SwiGLU
-from .modeling import (CausalLMOutput, ComplexityConfig, ComplexityModel, ModelOutput, SIZE_PRESETS,
+from .modeling import (CausalLMOutput, ComplexityConfig, ComplexityModel, GraphedForward, ModelOutput, SIZE_PRESETS,
                        count_parameters, create_complexity_model)
 from .normalization import (FusedResidualRMSNorm, RMSNorm, fused_add_rmsnorm_inplace, fused_residual_rmsnorm,
                             fused_rmsnorm)
@@ -32,7 +32,7 @@ __version__ = "1.0.0"
 __all__ = [
     "RMSNorm", "RotaryEmbedding", "apply_rotary_pos_emb", "ComplexityAttention", "MuGuidedAttention",
     "SwiGLU", "TokenRoutedMLP", "TransformerBlock", "MuGuidance", "ComplexityConfig", "ComplexityModel",
-    "CausalLMOutput", "ModelOutput", "create_complexity_model", "count_parameters", "SIZE_PRESETS",
+    "CausalLMOutput", "ModelOutput", "GraphedForward", "create_complexity_model", "count_parameters", "SIZE_PRESETS",
     "fused_residual_rmsnorm", "fused_add_rmsnorm_inplace", "fused_rmsnorm", "FusedResidualRMSNorm",
     "sort_tokens_by_expert", "sort_tokens_by_expert_fast", "cggr_grouped_gemm", "cggr_grouped_gemm_triton",
     "grouped_gemm_pytorch", "persistent_cggr_gemm", "persistent_swiglu_cggr", "fused_swiglu_triton",

@@ -125,3 +125,15 @@ def test_oracle_rope_frequencies_are_the_constructor_ones(oracle):
         rot = RotaryEmbedding(dim, theta=theta)
         assert torch.equal(oracle.rope_inv_freq(dim, theta), rot.inv_freq)
     assert math.isclose(float(oracle.rope_inv_freq(128)[1]), 10000.0 ** (-2 / 128), rel_tol=1e-6)
+
+
+def test_graphed_forward_needs_gpu_eval_model():
+    """GraphedForward refuses a model in training mode and a model on the host."""
+    import complexity_deep as cdx
+    cfg = cdx.ComplexityConfig(vocab_size=64, hidden_size=64, intermediate_size=128, num_hidden_layers=1,
+                               num_attention_heads=2, num_key_value_heads=1, num_experts=2)
+    m = cdx.ComplexityModel(cfg)
+    with pytest.raises(ValueError, match="eval mode"):
+        cdx.GraphedForward(m.train(), 1, 8)
+    with pytest.raises(ValueError, match="needs a GPU model"):
+        cdx.GraphedForward(m.eval(), 1, 8)
