@@ -86,6 +86,11 @@ def test_cfg4_1b_forward(cdx, oracle):
     with torch.no_grad():
         logits = m(ids.cuda()).logits
     assert logits.shape == (8, 2048, cfg.vocab_size)
+    # The same forward replayed from a recorded HIP graph gives the same bits.
+    graphed = m.capture_forward(8, 2048)
+    with torch.inference_mode():
+        assert torch.equal(graphed(ids.cuda()), logits), "graph replay differs from the eager 1B forward"
+    del graphed
     seq0 = logits[:1].float().cpu()
     assert torch.isfinite(logits).all()
     sd = _fp32_state(m)
