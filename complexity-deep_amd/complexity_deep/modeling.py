@@ -356,18 +356,19 @@ class GraphedForward:
     buffer, replays, and returns the graph's logits tensor, which the next call
     overwrites.  Inference only (no labels, mask or KV cache)."""
 
-    def __init__(self, model: "ComplexityModel", batch_size: int, seq_len: int,
-                 device: Optional[torch.device] = None, warmup: int = 2):
+    def __init__(self, model: "ComplexityModel", batch_size: int, seq_len: int, warmup: int = 2):
         if model.training:
             raise ValueError("GraphedForward: the model must be in eval mode")
-        dev = torch.device(device) if device is not None else next(model.parameters()).device
+        dev = next(model.parameters()).device
         if dev.type != "cuda":
             raise ValueError(f"GraphedForward: needs a GPU model, got {dev}")
+        if batch_size <= 0 or seq_len <= 0:
+            raise ValueError(f"GraphedForward: bad input shape ({batch_size}, {seq_len})")
         self.model = model
         self.shape = (int(batch_size), int(seq_len))
         self.input_ids = torch.zeros(self.shape, dtype=torch.long, device=dev)
         self.graph = torch.cuda.CUDAGraph()
-        with torch.inference_mode():
+        with torch.cuda.device(dev), torch.inference_mode():
             # Warm-up on a side stream (packs the weights, builds the RoPE tables), then
             # record one forward.
             side = torch.cuda.Stream(device=dev)
@@ -383,7 +384,8 @@ class GraphedForward:
         if tuple(input_ids.shape) != self.shape:
             raise ValueError(f"GraphedForward: captured for input shape {self.shape}, got {tuple(input_ids.shape)}")
         self.input_ids.copy_(input_ids)
-        self.graph.replay()
+        with torch.cuda.device(self.input_ids.device):
+            self.graph.replay()
         return self.logits
 
 
