@@ -14,17 +14,17 @@ import torch
 pytestmark = pytest.mark.gpu
 
 
-def test_graphed_forward_matches_eager(cdx):
+@pytest.mark.parametrize("shared,mu,B,S", [(True, True, 4, 512), (False, True, 2, 300), (True, False, 1, 77)])
+def test_graphed_forward_matches_eager(cdx, shared, mu, B, S):
     from complexity_deep import synthetic as syn
     cfg = cdx.ComplexityConfig(vocab_size=32000, hidden_size=768, intermediate_size=2048, num_hidden_layers=4,
-                               num_attention_heads=12, num_key_value_heads=4, num_experts=4, shared_expert=True,
-                               use_mu_guidance=True)
+                               num_attention_heads=12, num_key_value_heads=4, num_experts=4, shared_expert=shared,
+                               use_mu_guidance=mu)
     torch.manual_seed(0)
     m = cdx.ComplexityModel(cfg)
     syn.install_expert_map(m, syn.binpacked_map(cfg.vocab_size, cfg.num_experts))
     m = m.to("cuda", torch.bfloat16).eval()
-    B, S = 4, 512
-    print("graphed forward: README model with 4 layers, 4 x 512", flush=True)
+    print(f"graphed forward: README model with 4 layers, shared={shared} mu={mu}, {B} x {S}", flush=True)
     graphed = m.capture_forward(B, S)
     with torch.inference_mode():
         for seed in (0, 1, 2, 0):
