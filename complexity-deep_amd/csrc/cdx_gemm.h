@@ -134,7 +134,7 @@ struct GemmCfg {
   static constexpr int BN = BN_, BK = BK_, STAGES = STAGES_, MINB = MINB_;
   static constexpr int DMA_EVERY = DMA_EVERY_, DMA_OFF = DMA_OFF_, READ_EVERY = READ_EVERY_;
   static_assert(DMA_OFF < DMA_EVERY, "DMA slot offset must be below its spacing");
-  static_assert(BN == 256 || BN == 128, "BN must be 128 or 256");
+  static_assert(BN == 256 || BN == 128 || BN == 64, "BN must be 64, 128 or 256");
   static_assert(BK == 64, "BK must be 64 (two K32 sub-steps per stage)");
   static constexpr int STAGE_BYTES = (kBM + BN) * BK * 2;
   static_assert(STAGES >= 2 && STAGES * STAGE_BYTES * MINB <= 160 * 1024, "stages must fit 160 KB of LDS");

@@ -20,6 +20,11 @@ namespace {
 // Their K steps are half as long, so three stages (144 KB) give each load two steps
 // to land; refills ride behind every fourth MFMA of the step.
 using NarrowCfg = GemmCfg<128, 64, 3, 1, 4, 1, 1>;
+// Tiles of 256 x 64 for the plain epilogues (store, bias-clamp, scatter) of products
+// that leave most CUs idle even with 256 x 128 tiles; the SwiGLU and QK-norm epilogues
+// need a wave's 64 or more columns together.  Their ten refills per step ride behind
+// every second MFMA.
+using XNarrowCfg = GemmCfg<64, 64, 3, 1, 2, 1, 1>;
 
 template <ALoad AL, Epi EP, class Cfg = DefaultCfg, int HD = 0>
 int launch(GemmParams p, hipStream_t s, const char* name) {
@@ -31,6 +36,9 @@ int launch(GemmParams p, hipStream_t s, const char* name) {
   // (A head of 128 columns does not fit a narrow tile's 64-column waves.)
   if constexpr (Cfg::BN == 256 && (EP != Epi::kQKRope || HD <= 64)) {
     if (2 * nb <= device_cu_count()) return launch<AL, EP, NarrowCfg, HD>(p, s, name);
+  }
+  if constexpr (Cfg::BN == 128 && EP != Epi::kQKRope && EP != Epi::kSwiGLU) {
+    if (2 * nb <= device_cu_count()) return launch<AL, EP, XNarrowCfg, HD>(p, s, name);
   }
   if (nb > INT32_MAX) return fail(CDX_EUNSUPPORTED, "%s: problem too large (%lld tiles)", name, (long long)nb);
   // The kernel's K loop runs at least once and whole steps only.
