@@ -73,13 +73,15 @@ def test_persistent_mu_guidance_many_tiles(cdx):
 
 @pytest.mark.parametrize("K,N", [(768, 768), (2048, 2048), (1536, 1280)])
 def test_tile_forms_agree_bit_for_bit(cdx, K, N):
-    """The engine picks its tile form from the tile count: 256 x 128 tiles when at most
-    half as many 256 x 256 tiles as CUs, one 256 x 256 tile per block up to one per CU,
-    the persistent form beyond.  Every form accumulates an output element over K in the
-    same order, so rows are independent of the form: the first rows of a large product
-    (persistent) equal the product of those rows alone (narrow tiles) and of a middling
-    batch (one tile per block), bit for bit.  Checked for the plain product, the mu-QKV
-    contraction (two K sources) and mu guidance (bias + clamp)."""
+    """The engine picks its tile form from the tile count: 256 x 64 tiles (plain
+    epilogues) when even 256 x 128 tiles number at most half the CUs, 256 x 128 tiles
+    when at most half as many 256 x 256 tiles as CUs, one 256 x 256 tile per block up to
+    one per CU, the persistent form beyond.  Every form accumulates an output element
+    over K in the same order, so rows are independent of the form: the first rows of a
+    large product (persistent) equal the product of those rows alone (256 x 64 tiles),
+    of about 96 tiles' worth (256 x 128) and of a middling batch (one tile per block),
+    bit for bit.  Checked for the plain product, the mu-QKV contraction (two K sources)
+    and mu guidance (bias + clamp)."""
     from complexity_deep.attention import mu_qkv_project
     from complexity_deep.layer import mu_guidance
     from complexity_deep.linear import linear
@@ -88,16 +90,17 @@ def test_tile_forms_agree_bit_for_bit(cdx, K, N):
     nt = (N + 255) // 256
     big = 65536 if N <= 1280 else 32768  # far more 256 x 256 tiles than CUs: persistent
     mid = 256 * (192 // nt)              # about 192 tiles (256 CUs): one tile per block
+    nar = 256 * -(-96 // nt)             # about 96 tiles: 256 x 128 tiles
     x = torch.randn(big, K, generator=g).to(bf16).cuda()
     w = (torch.randn(N, K, generator=g) * 0.05).to(bf16).cuda()
     full = linear(x, w)
-    for rows in (256, mid):
+    for rows in (256, nar, mid):
         assert torch.equal(linear(x[:rows].contiguous(), w), full[:rows]), f"linear rows={rows}"
     H = K // 2
     mu = torch.randn(big, H, generator=g).clamp(-2, 2).to(bf16).cuda()
     wq = (torch.randn(N, 2 * H, generator=g) * 0.05).to(bf16).cuda()
     fq = mu_qkv_project(x[:, :H].contiguous().view(1, big, H), mu.view(1, big, H), wq, H)
-    for rows in (256, mid):
+    for rows in (256, nar, mid):
         part = mu_qkv_project(x[:rows, :H].contiguous().view(1, rows, H), mu[:rows].contiguous().view(1, rows, H),
                               wq, H)
         assert torch.equal(part, fq[:, :rows]), f"mu_qkv rows={rows}"
@@ -105,6 +108,6 @@ def test_tile_forms_agree_bit_for_bit(cdx, K, N):
         wm = (torch.randn(N, K, generator=g) * 0.02).to(bf16).cuda()
         bias = torch.linspace(0.0, 2.0, N, device="cuda")
         fm = mu_guidance(x, wm, bias, -2.0, 2.0)
-        for rows in (256, mid):
+        for rows in (256, nar, mid):
             assert torch.equal(mu_guidance(x[:rows].contiguous(), wm, bias, -2.0, 2.0), fm[:rows]), \
                 f"mu_guidance rows={rows}"
