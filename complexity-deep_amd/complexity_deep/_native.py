@@ -31,6 +31,9 @@ _SIGNATURES = {
     "cdx_route_workspace_bytes": (ctypes.c_size_t, [_i64, _i32]),
     "cdx_route_plan": (ctypes.c_int, [_vp, _i64, _vp, _i64, _i32, _vp, _vp, _vp, _vp, _vp, _vp,
                                       ctypes.c_size_t, _vp]),
+    "cdx_route_plans_workspace_bytes": (ctypes.c_size_t, [_i64, _i32, _i32]),
+    "cdx_route_plans": (ctypes.c_int, [_vp, _i64, _vp, _i32, _i64, _i32, _vp, _vp, _vp, _vp, _vp, _vp,
+                                       ctypes.c_size_t, _vp]),
     "cdx_route_noalloc_scratch_bytes": (ctypes.c_size_t, []),
     "cdx_route_plan_noalloc": (ctypes.c_int, [_vp, _i64, _vp, _i64, _i32, _vp, _vp, _vp, _vp, _vp, _vp]),
     "cdx_permute_rows": (ctypes.c_int, [_vp, _vp, _i64, _i64, _vp, _vp]),
@@ -48,8 +51,8 @@ _SIGNATURES = {
                                            _vp, _i64, _vp]),
     "cdx_attention_fwd": (ctypes.c_int, [_vp, _vp, _vp, _i64, _i64, _i32, _i32, _i32, _i64, ctypes.c_float,
                                          _vp, _vp]),
-    "cdx_mu_guidance_fwd": (ctypes.c_int, [_vp, _i64, _i32, _vp, _vp, ctypes.c_float, ctypes.c_float, _vp,
-                                           _vp]),
+    "cdx_mu_guidance_fwd": (ctypes.c_int, [_vp, _i64, _i32, _vp, _vp, ctypes.c_float, ctypes.c_float,
+                                           ctypes.c_float, ctypes.c_float, _vp, _vp]),
     "cdx_binpack_map": (ctypes.c_int, [_vp, _i64, _i32, _vp]),
     "cdx_embedding_fwd": (ctypes.c_int, [_vp, _i64, _vp, _i64, _i32, _vp, _vp]),
     "cdx_linear_fwd": (ctypes.c_int, [_vp, _i64, _vp, _i64, _i64, _i32, _i32, _vp, _i64, _vp]),

@@ -1,11 +1,12 @@
 """Decoder block and mu guidance; interfaces of core/layer.py:28-190.
 
 ``TransformerBlock.forward`` keeps the reference signature and returns
-(hidden_states, new_kv, mu) with mu unclamped, as the reference does.  Inside, the residual add before the MLP's norm is the
-fused add+RMSNorm kernel.  ``ComplexityModel`` drives the blocks through
-``forward_fused``, which also fuses the add after the MLP with the *next* norm (the
-next layer's input norm or the final norm) and reuses one routing plan for all
-layers.
+(hidden_states, new_kv, mu) with mu unclamped, as the reference does.  Inside, the
+residual add before the MLP's norm is the fused add+RMSNorm kernel.
+``ComplexityModel`` drives the blocks through ``forward_fused``, where both residual
+adds run inside the kernels that produce the branch outputs (o_proj as a GEMM with
+beta = 1, the MoE down pass in its scatter epilogue) and the norms after them are
+plain RMSNorms of h; the layer's routing plan comes from the model.
 """
 
 from __future__ import annotations
@@ -25,29 +26,33 @@ from .normalization import RMSNorm, add_rms_norm, rms_norm
 from .token_routed_mlp import RoutePlan, TokenRoutedMLP
 
 
-def mu_guidance(h: torch.Tensor, w: torch.Tensor, bias: torch.Tensor, lo: float = -math.inf,
-                hi: float = math.inf) -> torch.Tensor:
-    """clamp(h @ w^T + bias, lo, hi) through cdx_mu_guidance_fwd (fp32 accumulate, one
-    rounding).  h [..., H] bf16, w [H, H] bf16, bias [H] fp32."""
-    nat.require_device(h, w, what="mu_guidance")
+def mu_guidance(h: torch.Tensor, w: torch.Tensor, mu: torch.Tensor, mu_lo: float = -math.inf,
+                mu_hi: float = math.inf, lo: float = -math.inf, hi: float = math.inf) -> torch.Tensor:
+    """clamp(h @ w^T + clamp(mu, mu_lo, mu_hi), lo, hi) through cdx_mu_guidance_fwd (fp32
+    accumulate, one rounding).  h [..., H], w [H, H] and mu [H], all bf16."""
+    nat.require_device(h, w, mu, what="mu_guidance")
     H = h.shape[-1]
     h2 = h.reshape(-1, H)
     h2 = h2 if h2.is_contiguous() else h2.contiguous()
     w = w if w.is_contiguous() else w.contiguous()
+    mu = mu if mu.is_contiguous() else mu.contiguous()
+    if mu.shape != (H,):
+        raise ValueError(f"mu_guidance: mu must be [{H}], got {tuple(mu.shape)}")
     out = torch.empty(h.shape, dtype=h.dtype, device=h.device)
     with nat.launch_region("mu_guidance", h.device, T=h2.shape[0], H=H):
-        nat.check(nat.lib().cdx_mu_guidance_fwd(h2.data_ptr(), h2.shape[0], H, w.data_ptr(), bias.data_ptr(),
-                                                float(lo), float(hi), out.data_ptr(), nat.stream_of(h)),
-                  "cdx_mu_guidance_fwd")
+        nat.check(nat.lib().cdx_mu_guidance_fwd(h2.data_ptr(), h2.shape[0], H, w.data_ptr(), mu.data_ptr(),
+                                                float(mu_lo), float(mu_hi), float(lo), float(hi), out.data_ptr(),
+                                                nat.stream_of(h)), "cdx_mu_guidance_fwd")
     return out
 
 
 class MuGuidance(nn.Module):
     """mu = clamp(mu_param, mu_min, mu_max) + mu_proj(h); core/layer.py:28-61.
 
-    Runs as one kernel (cdx_mu_guidance_fwd): the mu_proj GEMM with the clamped
-    parameter added in its epilogue; ``fused(h, lo, hi)`` also applies the clamp the
-    model puts on mu between layers (models/modeling.py:199-200)."""
+    Runs as one kernel (cdx_mu_guidance_fwd): the mu_proj GEMM whose epilogue reads the
+    mu parameter, clamps it and adds it; ``fused(h, lo, hi)`` also applies the clamp the
+    model puts on mu between layers (models/modeling.py:199-200).  Nothing is cached:
+    the kernel reads both parameters on every call."""
 
     def __init__(self, hidden_size: int, mu_min: float = 0.0, mu_max: float = 2.0):
         super().__init__()
@@ -56,20 +61,10 @@ class MuGuidance(nn.Module):
         self.mu = nn.Parameter(torch.full((hidden_size,), (mu_min + mu_max) / 2))
         self.mu_proj = nn.Linear(hidden_size, hidden_size, bias=False)
         nn.init.zeros_(self.mu_proj.weight)
-        self._bias_key = None
-        self._bias = None
-
-    def _clamped_mu(self) -> torch.Tensor:
-        key = (self.mu.data_ptr(), self.mu._version, self.mu.device)
-        if key != self._bias_key:
-            with torch.no_grad():
-                self._bias = torch.clamp(self.mu.float(), self.mu_min, self.mu_max).contiguous()
-            self._bias_key = key
-        return self._bias
 
     def fused(self, hidden_states: torch.Tensor, lo: float = -math.inf, hi: float = math.inf) -> torch.Tensor:
         forward_only("MuGuidance", hidden_states, *self.parameters())
-        return mu_guidance(hidden_states, self.mu_proj.weight, self._clamped_mu(), lo, hi)
+        return mu_guidance(hidden_states, self.mu_proj.weight, self.mu, self.mu_min, self.mu_max, lo, hi)
 
     def forward(self, hidden_states: torch.Tensor) -> torch.Tensor:
         return self.fused(hidden_states)

@@ -32,22 +32,26 @@ def embedding(ids: torch.Tensor, table: torch.Tensor) -> torch.Tensor:
     return out.view(*ids.shape, H)
 
 
-def linear_supported(in_features: int, out_features: int) -> bool:
-    """Shapes cdx_linear_fwd takes: K a multiple of 64, N a multiple of 8."""
-    return in_features % 64 == 0 and out_features % 8 == 0
-
-
 def linear(x: torch.Tensor, w: torch.Tensor) -> torch.Tensor:
-    """x @ w^T for x [..., K], w [N, K] (nn.Linear weight layout), bf16."""
+    """x @ w^T for x [..., K], w [N, K] (nn.Linear weight layout), bf16; K a multiple of 64.
+
+    For N not a multiple of 8 the result is a view of the first N columns of a
+    [rows, round_up(N, 8)] buffer (the kernel stores whole 16-byte pieces); its leading
+    dimensions still merge (``.view(-1, N)`` works)."""
     nat.require_device(x, w, what="linear")
     N, K = w.shape
     if x.shape[-1] != K:
         raise ValueError(f"linear: x has {x.shape[-1]} features, weight expects {K}")
+    if K % 64 != 0:
+        raise ValueError(f"linear: in_features={K} must be a multiple of 64 (cdx_linear_fwd)")
     x2 = x.reshape(-1, K)
     x2 = x2 if x2.is_contiguous() else x2.contiguous()
     w = w if w.is_contiguous() else w.contiguous()
-    out = torch.empty(x2.shape[0], N, dtype=x.dtype, device=x.device)
+    n8 = (N + 7) // 8 * 8
+    out = torch.empty(x2.shape[0], n8, dtype=x.dtype, device=x.device)
     with nat.launch_region("lm_head", x.device, M=x2.shape[0], K=K, N=N):
-        nat.check(nat.lib().cdx_linear_fwd(x2.data_ptr(), K, w.data_ptr(), K, x2.shape[0], K, N, out.data_ptr(), N,
+        nat.check(nat.lib().cdx_linear_fwd(x2.data_ptr(), K, w.data_ptr(), K, x2.shape[0], K, N, out.data_ptr(), n8,
                                            nat.stream_of(x)), "cdx_linear_fwd")
+    if n8 != N:
+        out = out[:, :N]
     return out.view(*x.shape[:-1], N)

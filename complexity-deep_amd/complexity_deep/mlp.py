@@ -2,18 +2,19 @@
 
 Only used when ``use_token_routed_mlp=False``.  It runs on the same gfx950 kernel
 as the MoE (cdx_moe_swiglu_fwd) with one expert, no shared block and an identity
-routing plan, so the dense configuration also stays on MFMA.
+routing plan, so the dense configuration also stays on MFMA.  Its three nn.Linear
+weights are views of that kernel's operands (MLPOperands), as in TokenRoutedMLP.
 """
 
 from __future__ import annotations
 
-from typing import Optional
+from typing import Optional, Tuple
 
 import torch
 import torch.nn as nn
 
 from ._grad import forward_only
-from .token_routed_mlp import RoutePlan, moe_swiglu, pack_moe_weights
+from .token_routed_mlp import MLPOperands, RoutePlan, moe_swiglu
 from . import _native as nat
 
 
@@ -33,28 +34,21 @@ class SwiGLU(nn.Module):
         self.gate_proj = nn.Linear(hidden_size, intermediate_size, bias=False)
         self.up_proj = nn.Linear(hidden_size, intermediate_size, bias=False)
         self.down_proj = nn.Linear(intermediate_size, hidden_size, bias=False)
-        self._key = None
-        self._packed = None
+        self._operands = MLPOperands()
 
-    def refresh_packed_weights(self) -> None:
-        """Repack at the next forward (needed after writes through ``.data``, which bump
-        no version counter)."""
-        self._key = None
-        self._packed = None
+    def kernel_weights(self) -> Tuple[torch.Tensor, torch.Tensor]:
+        """(w_gu [1, 2, P, H], w_down [1, H, P]): the operands the three weights are views of."""
+        # One routed expert (block 0) whose weights are nn.Linear weights.
+        ws = {"lin_gate": self.gate_proj.weight, "lin_up": self.up_proj.weight, "lin_down": self.down_proj.weight}
+        I, H = self.gate_proj.weight.shape
+        return self._operands.get(ws, 1, H, I, False)
 
     def forward(self, x: torch.Tensor, residual: Optional[torch.Tensor] = None) -> torch.Tensor:
         """``residual`` (same shape, contiguous) receives residual + MLP(x) in place and is
         returned (the block's residual add fused into the down pass)."""
         forward_only("SwiGLU", x, residual, *self.parameters())
         nat.require_device(x, what="SwiGLU")
-        ws = (self.gate_proj.weight, self.up_proj.weight, self.down_proj.weight)
-        key = tuple((w.data_ptr(), w._version, w.dtype, w.device) for w in ws)
-        if key != self._key:
-            with torch.no_grad():
-                # [in, out] expert layout with E = 1
-                self._packed = pack_moe_weights(ws[0].t().unsqueeze(0), ws[1].t().unsqueeze(0),
-                                                ws[2].t().unsqueeze(0), None, None, None)
-            self._key = key
+        w_gu, w_down = self.kernel_weights()
         shape = x.shape
         x2d = x.reshape(-1, shape[-1]).contiguous()
         r2d = None
@@ -62,6 +56,6 @@ class SwiGLU(nn.Module):
             if residual.shape != shape or not residual.is_contiguous():
                 raise ValueError("SwiGLU: residual must be a contiguous tensor shaped like the input")
             r2d = residual.view(-1, shape[-1])
-        out = moe_swiglu(x2d, identity_plan(x2d.shape[0], x.device), *self._packed,
+        out = moe_swiglu(x2d, identity_plan(x2d.shape[0], x.device), w_gu, w_down,
                          self.gate_proj.weight.shape[0], False, residual=r2d)
         return out.view(shape)

@@ -7,18 +7,18 @@ and models/utils.py.
 state_dict keys and shapes match (modeling.py:69-149).
 
 The forward (modeling.py:155-219) runs the hot path on the gfx950 kernels:
-  * one routing plan per distinct expert map, computed once per forward and shared
-    by every layer using that map (the reference re-routes in each layer);
-  * a plain RMSNorm for layer 0's input, then every residual add fused with the
-    norm that follows it (2L fused add+RMSNorm calls, the last one being the final
-    norm);
+  * every routed layer gets its own routing plan through its own expert map, all of
+    them computed by one call (cdx_route_plans) at the top of the forward;
+  * both residual adds of every block run inside the kernels that produce the
+    branch outputs (o_proj as a hipBLASLt GEMM with beta = 1, the MoE down pass in
+    its scatter epilogue), and every norm (each layer's two, the final one) is a
+    plain RMSNorm of h;
   * the mu-QKV projection carries QK-norm and RoPE in its epilogue and feeds the
     causal GQA attention kernel (no mask, no KV cache);
   * mu guidance is one kernel that also applies the [-2, 2] clamp between layers;
   * the last layer's mu, which the reference computes and discards, is skipped;
   * the embedding gather and the tied LM head run on their own kernels
-    (cdx_embedding_fwd, cdx_linear_fwd; vocabularies not a multiple of 8 keep
-    nn.Linear for the head).
+    (cdx_embedding_fwd, cdx_linear_fwd, for any vocabulary size).
 o_proj runs as a PyTorch-ROCm op, as does attention with a mask or a KV cache
 (generation).
 """
@@ -37,9 +37,9 @@ import torch.nn.functional as F
 
 from ._grad import forward_only
 from .layer import TransformerBlock
-from .linear import embedding, linear, linear_supported
+from .linear import embedding, linear
 from .normalization import RMSNorm, rms_norm
-from .token_routed_mlp import RoutePlan, TokenRoutedMLP, route_plan
+from .token_routed_mlp import RoutePlan, TokenRoutedMLP, route_plans
 
 
 @dataclass
@@ -147,8 +147,6 @@ class ComplexityModel(nn.Module):
             self.mu_init = nn.Parameter(torch.zeros(1, 1, config.hidden_size))
         self.apply(self._init_weights)
         self._init_residual_scaling()
-        self._map_groups: List[int] = []
-        self._map_key = None
 
     # ---- initialisation (modeling.py:117-149) --------------------------------
     def _init_weights(self, module: nn.Module) -> None:
@@ -173,27 +171,13 @@ class ComplexityModel(nn.Module):
                 nn.init.normal_(mlp.shared_down.weight, mean=0.0, std=std)
 
     # ---- routing plans ---------------------------------------------------------
-    def _map_grouping(self) -> List[int]:
-        """Index of the first layer whose expert map equals each layer's map.
-
-        Re-evaluated only when a map buffer is replaced or modified (it compares
-        maps on the device, which synchronises once at that point)."""
-        maps = [layer.mlp.token_to_expert if layer.use_token_routed_mlp else None for layer in self.layers]
-        key = tuple(None if m is None else (m.data_ptr(), m._version, m.device) for m in maps)
-        if key != self._map_key:
-            canon: List[int] = []
-            for i, m in enumerate(maps):
-                owner = i
-                if m is not None:
-                    for j in range(i):
-                        if canon[j] == j and maps[j] is not None and maps[j].shape == m.shape \
-                                and torch.equal(maps[j], m):
-                            owner = j
-                            break
-                canon.append(owner)
-            self._map_groups = canon
-            self._map_key = key
-        return self._map_groups
+    def routing_maps(self) -> List[Tuple[int, torch.Tensor]]:
+        """(layer index, that layer's own token_to_expert buffer) for every routed layer:
+        the maps the forward routes through, looked up afresh on every call as the
+        reference does per layer (core/token_routed_mlp.py:149-150), so a write to any
+        one layer's map, however made, takes effect at the next forward."""
+        return [(i, layer.mlp.token_to_expert) for i, layer in enumerate(self.layers)
+                if layer.use_token_routed_mlp]
 
     def set_token_frequencies(self, token_frequencies: torch.Tensor) -> torch.Tensor:
         """Build the greedy bin-packing map of ``token_frequencies`` ([vocab] corpus
@@ -212,28 +196,18 @@ class ComplexityModel(nn.Module):
                 mlp.token_to_expert.copy_(tmap.to(mlp.token_to_expert.device))
         return tmap
 
-    def refresh_packed_weights(self) -> None:
-        """Repack the MLP weights of every layer at the next forward.  Needed only after
-        writes through ``.data`` to MLP weights (they bump no version counter); the
-        attention projections need nothing, their weights are views of the kernel's
-        operands."""
-        for layer in self.layers:
-            fn = getattr(layer.mlp, "refresh_packed_weights", None)
-            if fn is not None:
-                fn()
-
     def route_plans(self, input_ids: torch.Tensor) -> List[Optional[RoutePlan]]:
-        groups = self._map_grouping()
-        plans: Dict[int, RoutePlan] = {}
-        out: List[Optional[RoutePlan]] = []
-        for i, layer in enumerate(self.layers):
-            if not layer.use_token_routed_mlp:
-                out.append(None)
-                continue
-            g = groups[i]
-            if g not in plans:
-                plans[g] = route_plan(input_ids, layer.mlp.token_to_expert, layer.mlp.num_experts)
-            out.append(plans[g])
+        """One routing plan per routed layer, each through the layer's own map: every
+        plan of the forward in one cdx_route_plans call (two launches), with no host
+        synchronisation.  Layers whose MLPs differ in expert count or vocabulary get
+        a call per kind."""
+        out: List[Optional[RoutePlan]] = [None] * len(self.layers)
+        kinds: Dict[Tuple[int, int], List[Tuple[int, torch.Tensor]]] = {}
+        for i, m in self.routing_maps():
+            kinds.setdefault((self.layers[i].mlp.num_experts, m.shape[0]), []).append((i, m))
+        for (E, _), entries in kinds.items():
+            for (i, _), plan in zip(entries, route_plans(input_ids, [m for _, m in entries], E)):
+                out[i] = plan
         return out
 
     # ---- forward (modeling.py:155-219) --------------------------------------------
@@ -262,9 +236,7 @@ class ComplexityModel(nn.Module):
                 mu_prev = mu  # clamped to [-2, 2] inside the mu-guidance kernel
             if use_cache:
                 new_kvs.append(new_kv)
-        w_head = self.lm_head.weight
-        logits = linear(normed, w_head) if linear_supported(w_head.shape[1], w_head.shape[0]) \
-            else self.lm_head(normed)
+        logits = linear(normed, self.lm_head.weight)
         loss = None
         if labels is not None:
             loss = F.cross_entropy(logits[..., :-1, :].contiguous().view(-1, self.config.vocab_size),
@@ -350,9 +322,14 @@ class GraphedForward:
     replay issues the same kernels, in the same order and on the same buffers, from
     the device's queue, so results are the same bits as the eager forward.
 
-    Capture when the weights and the expert map are final: the graph reads the
-    kernel-layout weights and the map where they were at capture, so capture again
-    after changing either.  Each call copies ``input_ids`` into the graph's input
+    The graph reads every weight and expert map where it was at capture.  Values
+    written there later (in place, through ``.data``, by load_state_dict) are seen by
+    the next replay, since the kernels read the Parameters' own storage.  Storage that
+    moves (a cast or a move of the model, a Parameter or buffer replaced or given new
+    ``.data``) is not: each call checks that every parameter and buffer still has the
+    address it had at capture and raises if one moved (capture again then).  The
+    graph holds references to everything it reads, so nothing it replays from can be
+    freed while it lives.  Each call copies ``input_ids`` into the graph's input
     buffer, replays, and returns the graph's logits tensor, which the next call
     overwrites.  Inference only (no labels, mask or KV cache)."""
 
@@ -379,10 +356,24 @@ class GraphedForward:
             torch.cuda.current_stream(dev).wait_stream(side)
             with torch.cuda.graph(self.graph):
                 self.logits = model(self.input_ids).logits
+        # What the replays read: the parameters and buffers (the kernel operands are
+        # their storage), the MoE operands and the RoPE tables.
+        self._tensors = self._live_tensors()
+        self._ptrs = [t.data_ptr() for t in self._tensors]
+        self._keep = [m._operands.bufs for m in model.modules() if hasattr(m, "_operands")] + \
+                     [m._cs_table for m in model.modules() if getattr(m, "_cs_table", None) is not None] + \
+                     [m._qkv_w.buf for m in model.modules() if getattr(m, "_qkv_w", None) is not None]
+
+    def _live_tensors(self):
+        return list(self.model.parameters()) + list(self.model.buffers())
 
     def __call__(self, input_ids: torch.Tensor) -> torch.Tensor:
         if tuple(input_ids.shape) != self.shape:
             raise ValueError(f"GraphedForward: captured for input shape {self.shape}, got {tuple(input_ids.shape)}")
+        live = self._live_tensors()
+        if len(live) != len(self._ptrs) or any(t.data_ptr() != p for t, p in zip(live, self._ptrs)):
+            raise RuntimeError("GraphedForward: a parameter or buffer of the model has moved since capture "
+                               "(cast, moved, replaced or re-bound); capture the forward again")
         self.input_ids.copy_(input_ids)
         with torch.cuda.device(self.input_ids.device):
             self.graph.replay()

@@ -15,15 +15,17 @@ Interfaces follow the reference:
 The forward is: route plan (cdx_route_plan: expert lookup, counts, offsets, stable
 permutation) -> cdx_moe_swiglu_fwd (gathered gate/up GEMM with SwiGLU epilogue,
 then the down GEMM whose epilogue scatters rows back to token order).  The shared
-expert's weights are packed next to every routed expert's, so one fp32 accumulator
-sums shared + routed before the single bf16 rounding.  No host synchronisation
-happens anywhere in the forward.
+expert's columns are part of every token's product, so one fp32 accumulator sums
+shared + routed before the single bf16 rounding.  The module's weights are views of
+the two operands the kernels read (MLPOperands), so the kernels always see the live
+weights.  No host synchronisation happens anywhere in the forward.
 """
 
 from __future__ import annotations
 
+import ctypes
 from dataclasses import dataclass
-from typing import Optional, Tuple
+from typing import List, Optional, Sequence, Tuple
 
 import torch
 import torch.nn as nn
@@ -86,6 +88,45 @@ def route_plan(ids: torch.Tensor, token_map: Optional[torch.Tensor], num_experts
     return RoutePlan(expert_id, perm, inv_perm, counts, offsets, num_experts)
 
 
+def route_plans(ids: torch.Tensor, token_maps: Sequence[torch.Tensor], num_experts: int) -> List[RoutePlan]:
+    """One bit-exact routing plan per map over the same ids (cdx_route_plans): plan y
+    routes through token_maps[y], all of them in the same two launches.  Every map is
+    int64 [V] with one V for all; ids as in route_plan.  Plan y's tensors are rows of
+    [L, ...] buffers and equal route_plan(ids, token_maps[y], num_experts)."""
+    L = len(token_maps)
+    if L == 0:
+        return []
+    nat.require_device(ids, *token_maps, dtype=None, what="route_plans")
+    V = token_maps[0].shape[0]
+    maps = []
+    for m in token_maps:
+        if m.dim() != 1 or m.shape[0] != V:
+            raise ValueError(f"route_plans: every map must be [{V}], got {tuple(m.shape)}")
+        m = m if m.dtype == torch.int64 else m.to(torch.int64)
+        maps.append(m if m.is_contiguous() else m.contiguous())
+    ids = ids.reshape(-1)
+    ids = ids if ids.dtype == torch.int64 else ids.to(torch.int64)
+    ids = ids if ids.is_contiguous() else ids.contiguous()
+    T = ids.shape[0]
+    dev = ids.device
+    i32 = dict(dtype=torch.int32, device=dev)
+    expert_id = torch.empty(L, T, **i32)
+    perm = torch.empty(L, T, **i32)
+    inv_perm = torch.empty(L, T, **i32)
+    counts = torch.empty(L, num_experts, **i32)
+    offsets = torch.empty(L, num_experts + 1, **i32)
+    lib = nat.lib()
+    ws_bytes = lib.cdx_route_plans_workspace_bytes(T, num_experts, L)
+    ws = torch.empty(max(ws_bytes, 16), dtype=torch.uint8, device=dev)
+    table = (ctypes.c_void_p * L)(*[m.data_ptr() for m in maps])
+    with nat.launch_region("route_plan", dev, T=T, E=num_experts, V=V, L=L):
+        nat.check(lib.cdx_route_plans(ids.data_ptr(), T, ctypes.cast(table, ctypes.c_void_p), L, V, num_experts,
+                                      expert_id.data_ptr(), perm.data_ptr(), inv_perm.data_ptr(),
+                                      counts.data_ptr(), offsets.data_ptr(), ws.data_ptr(), ws_bytes,
+                                      nat.stream_of(ids)), "cdx_route_plans")
+    return [RoutePlan(expert_id[y], perm[y], inv_perm[y], counts[y], offsets[y], num_experts) for y in range(L)]
+
+
 def _aligned_rows(t: torch.Tensor) -> torch.Tensor:
     """Contiguous with a 16-byte aligned base (the kernels' DMA needs both)."""
     t = t.contiguous()
@@ -122,8 +163,6 @@ def sort_tokens_by_expert(tokens: torch.Tensor, expert_ids: torch.Tensor, num_ex
     nat.require_device(tokens, expert_ids, dtype=None, what="sort_tokens_by_expert")
     plan = route_plan(expert_ids, None, num_experts)
     rows = tokens.reshape(tokens.shape[0], -1)
-    if (rows.shape[1] * rows.element_size()) % 16 != 0:
-        raise ValueError("sort_tokens_by_expert: token rows must be a multiple of 16 bytes")
     sorted_tokens = permute_rows(rows, plan.perm).view_as(tokens)
     return sorted_tokens, plan.perm.to(torch.int64), plan.offsets.to(torch.int64), plan.counts.to(torch.int64)
 
@@ -219,48 +258,94 @@ def fused_swiglu_simple(gate: torch.Tensor, up: torch.Tensor) -> torch.Tensor:
 
 
 # ---------------------------------------------------------------------------
-# weight packing (layouts documented in include/cdx.h, cdx_moe_swiglu_fwd)
+# weight operands (layouts documented in include/cdx.h, cdx_moe_swiglu_fwd)
 # ---------------------------------------------------------------------------
 
 def padded_width(ie: int) -> int:
     return (ie + 63) // 64 * 64
 
 
-def _interleave_gate_up(gate_rows: torch.Tensor, up_rows: torch.Tensor, P: int) -> torch.Tensor:
-    """[Ie, H] gate and up rows -> [2P, H]: groups of 32 gate rows then the matching 32 up rows."""
-    ie, H = gate_rows.shape
-    g = torch.zeros(P, H, dtype=gate_rows.dtype, device=gate_rows.device)
-    u = torch.zeros_like(g)
-    g[:ie] = gate_rows
-    u[:ie] = up_rows
-    return torch.stack([g.view(P // 32, 32, H), u.view(P // 32, 32, H)], dim=1).reshape(2 * P, H)
+def operand_views(w_gu: torch.Tensor, w_down: torch.Tensor, ie: int, has_shared: bool) -> dict:
+    """The parameter-shaped views of the kernel operands w_gu [NB, 2, P, H] and
+    w_down [NB, H, P] (block 0 the shared expert when has_shared):
+      gate / up   [E, H, Ie]  routed gate_proj_w / up_proj_w ([in, out])
+      down        [E, Ie, H]  routed down_proj_w ([in, out])
+      lin_gate / lin_up [Ie, H], lin_down [H, Ie]   block 0 as nn.Linear weights
+                              ([out, in]): the shared expert's, or the dense SwiGLU's
+      shared_gate / shared_up / shared_down         the lin_* views, when has_shared"""
+    s0 = 1 if has_shared else 0
+    v = {"gate": w_gu[s0:, 0, :ie, :].transpose(1, 2), "up": w_gu[s0:, 1, :ie, :].transpose(1, 2),
+         "down": w_down[s0:, :, :ie].transpose(1, 2),
+         "lin_gate": w_gu[0, 0, :ie, :], "lin_up": w_gu[0, 1, :ie, :], "lin_down": w_down[0, :, :ie]}
+    if has_shared:
+        v.update(shared_gate=v["lin_gate"], shared_up=v["lin_up"], shared_down=v["lin_down"])
+    return v
+
+
+def new_operands(E: int, H: int, ie: int, has_shared: bool, dtype, device) -> Tuple[torch.Tensor, torch.Tensor]:
+    """Zeroed kernel operands (w_gu [NB, 2, P, H], w_down [NB, H, P]) for E experts."""
+    P = padded_width(ie)
+    nb = E + (1 if has_shared else 0)
+    return (torch.zeros(nb, 2, P, H, dtype=dtype, device=device),
+            torch.zeros(nb, H, P, dtype=dtype, device=device))
 
 
 def pack_moe_weights(gate_w: torch.Tensor, up_w: torch.Tensor, down_w: torch.Tensor,
                      shared_gate: Optional[torch.Tensor], shared_up: Optional[torch.Tensor],
                      shared_down: Optional[torch.Tensor]) -> Tuple[torch.Tensor, torch.Tensor]:
-    """Build (w_gu [E, S*2P, H], w_down [E, H, S*P]) from the module's parameters.
-
-    gate_w/up_w [E, H, Ie] and down_w [E, Ie, H] are [in, out]; shared_* are
-    nn.Linear weights [out, in]."""
+    """Fresh (w_gu, w_down) operands holding copies of the given weights: gate_w/up_w
+    [E, H, Ie] and down_w [E, Ie, H] are [in, out]; shared_* are nn.Linear weights
+    [out, in] (or None).  One strided copy per weight."""
     E, H, ie = gate_w.shape
-    P = padded_width(ie)
     has_shared = shared_gate is not None
-    blocks_gu, blocks_dn = [], []
+    w_gu, w_down = new_operands(E, H, ie, has_shared, gate_w.dtype, gate_w.device)
+    views = operand_views(w_gu, w_down, ie, has_shared)
     with torch.no_grad():
+        views["gate"].copy_(gate_w)
+        views["up"].copy_(up_w)
+        views["down"].copy_(down_w)
         if has_shared:
-            sg = _interleave_gate_up(shared_gate, shared_up, P)  # [2P, H]
-            sd = torch.zeros(H, P, dtype=down_w.dtype, device=down_w.device)
-            sd[:, :ie] = shared_down
-        for e in range(E):
-            rg = _interleave_gate_up(gate_w[e].t(), up_w[e].t(), P)
-            rd = torch.zeros(H, P, dtype=down_w.dtype, device=down_w.device)
-            rd[:, :ie] = down_w[e].t()
-            blocks_gu.append(torch.cat([sg, rg], 0) if has_shared else rg)
-            blocks_dn.append(torch.cat([sd, rd], 1) if has_shared else rd)
-        w_gu = torch.stack(blocks_gu).contiguous()
-        w_down = torch.stack(blocks_dn).contiguous()
+            views["shared_gate"].copy_(shared_gate)
+            views["shared_up"].copy_(shared_up)
+            views["shared_down"].copy_(shared_down)
     return w_gu, w_down
+
+
+class MLPOperands:
+    """The MoE kernel operands of one MLP module, w_gu [NB, 2, P, H] and
+    w_down [NB, H, P], whose slices the module's weight Parameters are views of.
+
+    Every write to a weight (in place, through ``.data``, by load_state_dict) therefore
+    lands in the operand the kernel reads, and nothing is cached that could go stale.
+    When a weight is no longer its view (the module was moved or cast, a Parameter was
+    replaced or given new ``.data``), ``get`` copies the current weights into new
+    operands and re-points the Parameters at them.  The operands are made outside
+    inference mode, so that the weights stay writable after a forward run under
+    torch.inference_mode()."""
+
+    def __init__(self):
+        self.bufs: Optional[Tuple[torch.Tensor, torch.Tensor]] = None
+        self.ptrs = None
+
+    def get(self, params: dict, E: int, H: int, ie: int, has_shared: bool) -> Tuple[torch.Tensor, torch.Tensor]:
+        """params maps the operand_views names to the module's Parameters."""
+        ws = list(params.values())
+        if self.bufs is None or [w.data_ptr() for w in ws] != self.ptrs:
+            dt, dev = ws[0].dtype, ws[0].device
+            if any(w.dtype != dt or w.device != dev for w in ws):
+                raise ValueError("MLP weights must share one dtype and device")
+            with torch.inference_mode(False), torch.no_grad():
+                bufs = new_operands(E, H, ie, has_shared, dt, dev)
+                views = operand_views(*bufs, ie, has_shared)
+                for name, w in params.items():
+                    if views[name].shape != w.shape:
+                        raise ValueError(f"MLP weight {name}: shape {tuple(w.shape)}, expected "
+                                         f"{tuple(views[name].shape)}")
+                    views[name].copy_(w)
+                    w.data = views[name]
+            self.bufs = bufs
+            self.ptrs = [w.data_ptr() for w in ws]
+        return self.bufs
 
 
 def moe_swiglu(x2d: torch.Tensor, plan: RoutePlan, w_gu: torch.Tensor, w_down: torch.Tensor,
@@ -277,9 +362,13 @@ def _moe_swiglu(x2d: torch.Tensor, perm: torch.Tensor, offsets: torch.Tensor, E:
                 ) -> torch.Tensor:
     T, H = x2d.shape
     P = padded_width(ie)
+    nb = E + (1 if has_shared else 0)
+    nat.require_device(x2d, w_gu, w_down, what="moe_swiglu")
+    if w_gu.shape != (nb, 2, P, H) or w_down.shape != (nb, H, P) or not (w_gu.is_contiguous()
+                                                                       and w_down.is_contiguous()):
+        raise ValueError("moe_swiglu: weight operands must be contiguous [NB, 2, P, H] and [NB, H, P] "
+                         f"for NB={nb}, P={P}, H={H}")
     S = 2 if has_shared else 1
-    if w_gu.shape != (E, 2 * S * P, H) or w_down.shape != (E, H, S * P):
-        raise ValueError("moe_swiglu: packed weight shapes do not match the plan/hidden size")
     if residual is not None:
         nat.require_device(residual, x2d, what="moe_swiglu residual")
         if residual.shape != x2d.shape or not residual.is_contiguous():
@@ -302,11 +391,13 @@ def persistent_swiglu_cggr(sorted_tokens: torch.Tensor, gate_weights: torch.Tens
 
     out[o_e:o_{e+1}] = (silu(t @ gate[e]) * (t @ up[e])) @ down[e] for t the rows of
     segment e, zero outside [offsets[0], offsets[E]).  gate/up [E, H, I] and down
-    [E, I, H] ([in, out], bf16).  Both GEMMs run on cdx_moe_swiglu_fwd with an
+    [E, I, H] ([in, out], bf16 only).  Both GEMMs run on cdx_moe_swiglu_fwd with an
     identity permutation and no shared block; the gate/up products stay fp32 into
     the SwiGLU, which is rounded once (the reference rounds the two products to bf16
-    first).  The weights are packed on every call, as the operator holds no state.
-    ``num_sms`` is accepted for API compatibility."""
+    first).  The operator holds no state, so the weights are copied into the kernel
+    layout on every call (three strided copies, about as many bytes as the GEMMs read;
+    a cache would miss writes made through ``.data``).  ``num_sms`` is accepted for
+    API compatibility."""
     forward_only("persistent_swiglu_cggr", sorted_tokens, gate_weights, up_weights, down_weights)
     nat.require_device(sorted_tokens, gate_weights, up_weights, down_weights, what="persistent_swiglu_cggr")
     if sorted_tokens.dim() != 2:
@@ -333,7 +424,9 @@ class TokenRoutedMLP(nn.Module):
 
     Same constructor, parameters ([E,H,Ie] gate/up, [E,Ie,H] down, nn.Linear shared
     expert), ``token_to_expert`` buffer and state_dict keys as
-    core/token_routed_mlp.py:43-81."""
+    core/token_routed_mlp.py:43-81.  From the first forward on, the six weight
+    Parameters are views of the kernel operands (MLPOperands): strided, not
+    contiguous, and read by the kernels on every call."""
 
     def __init__(self, hidden_size: int, intermediate_size: int, num_experts: int = 4,
                  vocab_size: int = 100_000, shared_expert: bool = True,
@@ -355,8 +448,7 @@ class TokenRoutedMLP(nn.Module):
             self.shared_down = nn.Linear(ie, hidden_size, bias=False)
         self.register_buffer("token_to_expert",
                              self._build_token_mapping(vocab_size, num_experts, token_frequencies))
-        self._pack_key = None
-        self._packed = None
+        self._operands = MLPOperands()
 
     @staticmethod
     def _build_token_mapping(vocab_size: int, num_experts: int,
@@ -375,29 +467,17 @@ class TokenRoutedMLP(nn.Module):
                   "cdx_binpack_map")
         return mapping
 
-    def refresh_packed_weights(self) -> None:
-        """Drop the kernel-layout copies, so the next forward packs the parameters anew.
-
-        In-place writes to a parameter bump its version and are picked up without this;
-        writes through ``.data`` (``p.data.zero_()``) bump no version counter and need
-        this call."""
-        self._pack_key = None
-        self._packed = None
-        self._all_key = None
-
-    def packed_weights(self) -> Tuple[torch.Tensor, torch.Tensor]:
-        """Kernel-layout weights, rebuilt only when a parameter changes (never saved)."""
-        params = [self.gate_proj_w, self.up_proj_w, self.down_proj_w]
+    def _weights(self) -> dict:
+        w = {"gate": self.gate_proj_w, "up": self.up_proj_w, "down": self.down_proj_w}
         if self.use_shared_expert:
-            params += [self.shared_gate.weight, self.shared_up.weight, self.shared_down.weight]
-        key = tuple((p.data_ptr(), p._version, p.dtype, p.device) for p in params)
-        if key != self._pack_key:
-            sh = (self.shared_gate.weight, self.shared_up.weight, self.shared_down.weight) \
-                if self.use_shared_expert else (None, None, None)
-            self._packed = pack_moe_weights(self.gate_proj_w.detach(), self.up_proj_w.detach(),
-                                            self.down_proj_w.detach(), *[None if t is None else t.detach() for t in sh])
-            self._pack_key = key
-        return self._packed
+            w.update(shared_gate=self.shared_gate.weight, shared_up=self.shared_up.weight,
+                     shared_down=self.shared_down.weight)
+        return w
+
+    def kernel_weights(self) -> Tuple[torch.Tensor, torch.Tensor]:
+        """(w_gu, w_down): the operands the kernels read, of which the weights are views."""
+        return self._operands.get(self._weights(), self.num_experts, self.hidden_size,
+                                  self.expert_intermediate_size, self.use_shared_expert)
 
     def plan(self, token_ids: torch.Tensor) -> RoutePlan:
         return route_plan(token_ids, self.token_to_expert, self.num_experts)
@@ -406,10 +486,10 @@ class TokenRoutedMLP(nn.Module):
                 route: Optional[RoutePlan] = None, residual: Optional[torch.Tensor] = None) -> torch.Tensor:
         """[B, S, H] -> [B, S, H] = SharedMLP(x) + Expert_{map[token_id]}(x).
 
-        ``route`` lets the caller pass a plan computed once for several layers that
-        share token ids and map (ComplexityModel does this).  ``residual`` (same shape,
-        contiguous) receives residual + MLP(x) in place and is returned: the block's
-        residual add (core/layer.py:183) fused into the down pass."""
+        ``route`` lets the caller pass the plan of this layer's map computed ahead
+        (ComplexityModel computes every layer's in one call).  ``residual`` (same
+        shape, contiguous) receives residual + MLP(x) in place and is returned: the
+        block's residual add (core/layer.py:183) fused into the down pass."""
         forward_only("TokenRoutedMLP", hidden_states, residual, *self.parameters())
         nat.require_device(hidden_states, what="TokenRoutedMLP")
         shape = hidden_states.shape
@@ -423,7 +503,7 @@ class TokenRoutedMLP(nn.Module):
             route = self.plan(token_ids)
         if route.num_tokens != x2d.shape[0]:
             raise ValueError(f"TokenRoutedMLP: plan has {route.num_tokens} tokens, input has {x2d.shape[0]}")
-        w_gu, w_down = self.packed_weights()
+        w_gu, w_down = self.kernel_weights()
         r2d = None
         if residual is not None:
             if residual.shape != shape or not residual.is_contiguous():
@@ -435,23 +515,18 @@ class TokenRoutedMLP(nn.Module):
 
     def _forward_all_experts(self, x2d: torch.Tensor) -> torch.Tensor:
         """token_ids=None: mean over all experts plus the shared expert
-        (token_routed_mlp.py:180-194).  Computed as one dense SwiGLU of width (E+1)*P
-        whose routed down-projection rows are scaled by 1/E."""
-        key = ("all",) + tuple((p.data_ptr(), p._version) for p in self.parameters())
-        if getattr(self, "_all_key", None) != key:
-            E = self.num_experts
-            sh = (self.shared_gate.weight, self.shared_up.weight, self.shared_down.weight) \
-                if self.use_shared_expert else None
-            with torch.no_grad():
-                gate = torch.cat(([sh[0].t()] if sh else []) + [self.gate_proj_w[e] for e in range(E)], 1)
-                up = torch.cat(([sh[1].t()] if sh else []) + [self.up_proj_w[e] for e in range(E)], 1)
-                down = torch.cat(([sh[2].t()] if sh else []) + [self.down_proj_w[e] / E for e in range(E)], 0)
-                self._all_packed = pack_moe_weights(gate.unsqueeze(0), up.unsqueeze(0), down.unsqueeze(0),
-                                                    None, None, None)
-            self._all_width = gate.shape[1]
-            self._all_key = key
+        (token_routed_mlp.py:180-194).  Computed as one dense SwiGLU of width (E+1)*Ie
+        whose routed down-projection rows are scaled by 1/E; its operands are built
+        from the current weights on every call (this path is not the model's)."""
+        E = self.num_experts
+        sh = (self.shared_gate.weight, self.shared_up.weight, self.shared_down.weight) \
+            if self.use_shared_expert else None
+        with torch.no_grad():
+            gate = torch.cat(([sh[0].t()] if sh else []) + [self.gate_proj_w[e] for e in range(E)], 1)
+            up = torch.cat(([sh[1].t()] if sh else []) + [self.up_proj_w[e] for e in range(E)], 1)
+            down = torch.cat(([sh[2].t()] if sh else []) + [self.down_proj_w[e] / E for e in range(E)], 0)
+            w_gu, w_down = pack_moe_weights(gate.unsqueeze(0), up.unsqueeze(0), down.unsqueeze(0), None, None, None)
         T = x2d.shape[0]
         ident = torch.arange(T, dtype=torch.int32, device=x2d.device)
         offsets = torch.arange(2, dtype=torch.int32, device=x2d.device) * T
-        w_gu, w_down = self._all_packed
-        return _moe_swiglu(x2d, ident, offsets, 1, w_gu, w_down, self._all_width, False)
+        return _moe_swiglu(x2d, ident, offsets, 1, w_gu, w_down, gate.shape[1], False)

@@ -97,9 +97,18 @@ struct GemmParams {
   int64_t M;
   // B operand: expert e uses b + e * b_estride, rows n with stride ldb
   const uint16_t* b;
-  const uint16_t* b2;  // concat: B columns [k_split, K) come from b2 (rows n, stride ldb)
+  // concat: B columns [k_split, K) come from b2 (rows n, stride ldb).
+  // Scatter epilogues (the MoE down pass): b2 is the shared expert's [N][ldb] block,
+  // which serves K columns [0, k_split); expert e serves [k_split, K) from its own
+  // block b + e * b_estride, whose column 0 is K column k_split.
+  const uint16_t* b2;
   int64_t ldb;
   int64_t b_estride;
+  // kSwiGLU (the MoE gate/up pass): b is the [blocks][2][gu_P][ldb] weights, gate rows
+  // then up rows of each block; block 0 is the shared expert when gu_shared, then one
+  // block per routed expert (gu_tile maps a tile's logical rows onto them).
+  int32_t gu_P;
+  int32_t gu_shared;
   int32_t N;
   int32_t K;
   // C
@@ -109,8 +118,9 @@ struct GemmParams {
   int32_t mt_count;  // number of M tiles (upper bound for grouped GEMMs)
   int32_t nt_count;
   QKRopeParams qk;  // kQKRope epilogue only
-  // kBiasClamp epilogue: c = clamp(acc + bias[n], lo, hi)
-  const float* bias;  // [N] fp32
+  // kBiasClamp epilogue: c = clamp(acc + clamp(bias[n], bias_lo, bias_hi), lo, hi)
+  const uint16_t* bias;  // [N] bf16
+  float bias_lo, bias_hi;
   float lo, hi;
 };
 
@@ -160,6 +170,15 @@ __device__ __forceinline__ int xcd_remap(int b, int tiles) {
 // bf16 afterwards.  exp(-g) overflowing to +inf gives rcp = 0 and silu = -0.
 __device__ __forceinline__ float silu_f32(float g) { return g * __builtin_amdgcn_rcpf(1.0f + __expf(-g)); }
 
+// Four bf16 bias values (8 bytes) as fp32, each clamped to [lo, hi] (the clamp on the
+// mu parameter, core/layer.py:60, applied where the epilogue reads it).
+__device__ __forceinline__ float4 load_bias4(const uint16_t* src, float lo, float hi) {
+  const uint2 w = *reinterpret_cast<const uint2*>(src);
+  auto cl = [&](float v) __attribute__((always_inline)) { return fminf(fmaxf(v, lo), hi); };
+  return make_float4(cl(__uint_as_float(w.x << 16)), cl(__uint_as_float(w.x & 0xffff0000u)),
+                     cl(__uint_as_float(w.y << 16)), cl(__uint_as_float(w.y & 0xffff0000u)));
+}
+
 // s_waitcnt immediate (gfx9 layout: vmcnt bits 3:0 and 15:14, expcnt 6:4, lgkmcnt 11:8).
 constexpr int waitcnt_imm(int vm, int lgkm) {
   return (vm & 15) | ((vm >> 4) << 14) | (7 << 4) | ((lgkm & 15) << 8);
@@ -179,6 +198,40 @@ __device__ __forceinline__ void buf_dma16(__amdgpu_buffer_rsrc_t r, uint32_t vof
                                           uint8_t* lds_block) {
   __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void*)lds_block, 16, voff, soff,
                                            0, 0);
+}
+
+// kSwiGLU B tiles.  Logical row n of expert e's gate/up operand (n < S * 2P, S = 2
+// with the shared expert, else 1) is in block n / (2P) of the expert's sequence
+// (shared block, then its own); inside it, w = n % (2P) is the gate (w / 32 even) or
+// up row of unit (w / 64) * 32 + w % 32, so that a tile's rows interleave 32 gate rows
+// with the 32 up rows of the same units.  Storage keeps gate and up rows in unit
+// order ([blocks][2][P][H]), which is what makes the module's weight Parameters views
+// of the operand.  For a tile starting at logical row n0 (a multiple of 128; P is a
+// multiple of 64), row r < BN sits at
+//     lo + gu_row(r) * ldb            for r <  split
+//     hi + gu_row(r) * ldb            for r >= split
+// with gu_row(r) = ((r / 32) % 2) * P + (r / 64) * 32 + r % 32 and split, a multiple of
+// 128, where the tile crosses into the next block (tiles past the last block read
+// rows of that block again: computed, never stored).  A DMA instruction's eight rows
+// never straddle split, so the choice of base is one scalar select per instruction.
+struct GuTile {
+  uintptr_t lo, hi;
+  int split;
+};
+__device__ __forceinline__ int gu_row(int r, int P) { return ((r >> 5) & 1) * P + (r >> 6) * 32 + (r & 31); }
+__device__ __forceinline__ GuTile gu_tile(const uint16_t* b, int64_t ldb, int P, bool shared, int e, int n0) {
+  const int twoP = 2 * P;
+  const int bl = n0 / twoP;
+  const int w0 = n0 - bl * twoP;
+  const int last = shared ? 1 : 0;
+  const int64_t blk_lo = shared && bl == 0 ? 0 : last + e;
+  const int64_t blk_hi = last + e;  // the next block, when bl == 0 and there is one
+  GuTile t;
+  t.split = twoP - w0;
+  t.lo = (uintptr_t)(b + (blk_lo * twoP + w0 / 2) * ldb);
+  t.hi = bl < last ? (uintptr_t)(b + (blk_hi * twoP - t.split / 2) * ldb)
+                   : (uintptr_t)(b + (blk_lo * twoP + w0 / 2 - t.split / 2) * ldb);
+  return t;
 }
 
 // ---- QK-norm + RoPE epilogue pieces (shared by the engine's two kernel forms) ----
@@ -378,6 +431,10 @@ __global__ __launch_bounds__(kGemmThreads, Cfg::MINB) void gemm_nt_kernel(const 
   // of K take the same scalar offset (2 k0) and the choice between the two sources is
   // a select, not a branch.
   const int dr = lane / CPR;
+  constexpr bool kGuTiles = EP == Epi::kSwiGLU;
+  // Scatter epilogues on per-expert tiles (the down pass, kDense): K columns below
+  // k_split come from the shared block b2.
+  constexpr bool kSharedB = kScatterRows && AL == ALoad::kDense;
   const uint16_t* bexp = p.b + (int64_t)e * p.b_estride;
   const uintptr_t a_base = (uintptr_t)(AL == ALoad::kGather ? p.a : p.a + m0 * p.lda);
   const uintptr_t a2_base =
@@ -387,10 +444,16 @@ __global__ __launch_bounds__(kGemmThreads, Cfg::MINB) void gemm_nt_kernel(const 
   const __amdgpu_buffer_rsrc_t rs_a =
       AL == ALoad::kSegmented ? make_rsrc((const void*)a_base, (uint32_t)((m_end - m0) * p.lda * 2))
                               : make_rsrc((const void*)a_base);
+  GuTile gu{};
+  if constexpr (kGuTiles) gu = gu_tile(p.b, p.ldb, p.gu_P, p.gu_shared != 0, e, n0);
   const __amdgpu_buffer_rsrc_t rs_b = make_rsrc(bexp + (int64_t)n0 * p.ldb);
-  const uintptr_t b_base = (uintptr_t)(bexp + (int64_t)n0 * p.ldb);
+  // kSharedB: b_base serves the expert columns (column 0 = K column k_split), b2_base
+  // the shared ones.
+  const uintptr_t b_base =
+      (uintptr_t)(bexp + (int64_t)n0 * p.ldb) - (kSharedB ? (uintptr_t)p.k_split * 2 : (uintptr_t)0);
   const uintptr_t b2_base =
-      AL == ALoad::kConcat ? (uintptr_t)(p.b2 + (int64_t)n0 * p.ldb) - (uintptr_t)p.k_split * 2 : b_base;
+      AL == ALoad::kConcat ? (uintptr_t)(p.b2 + (int64_t)n0 * p.ldb) - (uintptr_t)p.k_split * 2
+                           : (kSharedB && p.b2 != nullptr ? (uintptr_t)(p.b2 + (int64_t)n0 * p.ldb) : b_base);
   constexpr uint32_t kMaskedOff = 0x80000000u;
   uint32_t a_off[LD_A], a2_off[LD_A], b_off[LD_B];
   int a_exp[AL == ALoad::kSegmented ? LD_A : 1];
@@ -425,9 +488,13 @@ __global__ __launch_bounds__(kGemmThreads, Cfg::MINB) void gemm_nt_kernel(const 
   for (int j = 0; j < LD_B; ++j) {
     const int r = wave * (kBN / 4) + j * ROWS_PER_DMA + dr;
     const int dchunk = (lane % CPR) ^ ((r / RPL) % CPR);
-    int n = n0 + r;
-    n = n < p.N ? n : p.N - 1;
-    b_off[j] = (uint32_t)(((int64_t)(n - n0) * p.ldb + dchunk * 8) * 2);
+    if constexpr (kGuTiles) {
+      b_off[j] = (uint32_t)(((int64_t)gu_row(r, p.gu_P) * p.ldb + dchunk * 8) * 2);
+    } else {
+      int n = n0 + r;
+      n = n < p.N ? n : p.N - 1;
+      b_off[j] = (uint32_t)(((int64_t)(n - n0) * p.ldb + dchunk * 8) * 2);
+    }
   }
   const int a_dma_off = wave * (kBM / 4) * ROW_BYTES;  // this wave's first DMA block in A
   const int b_dma_off = A_TILE_BYTES + wave * (kBN / 4) * ROW_BYTES;
@@ -450,12 +517,13 @@ __global__ __launch_bounds__(kGemmThreads, Cfg::MINB) void gemm_nt_kernel(const 
   // selects instead of a division per step: the shared columns, then each expert's.
   StepSrc seg_next{ks0 > 0 ? 0 : p.k_split, ks0 > 0 ? -1 : e_lo, true};
   int seg_step = 0;
-  // B descriptor of the step's expert (the shared columns are packed with every
-  // expert's down weights; e_lo's serve), or the empty one past the end.
-  // Kept as an address, not as a descriptor: a loop-carried descriptor is not kept in
-  // scalar registers.
+  // B of the step: the shared block b2 for the shared columns, else the step's expert
+  // block (addressed so that K column k_split is its column 0), or the empty
+  // descriptor past the end.  Kept as addresses, not as descriptors: a loop-carried
+  // descriptor is not kept in scalar registers.
   const uintptr_t b_estep = (uintptr_t)p.b_estride * 2;
-  uintptr_t seg_bptr = (uintptr_t)(p.b + (int64_t)n0 * p.ldb + (int64_t)e_lo * p.b_estride);
+  const uintptr_t seg_sptr = AL == ALoad::kSegmented && p.b2 != nullptr ? (uintptr_t)(p.b2 + (int64_t)n0 * p.ldb) : 0;
+  uintptr_t seg_bptr = (uintptr_t)(p.b + (int64_t)n0 * p.ldb + (int64_t)e_lo * p.b_estride) - (uintptr_t)p.k_split * 2;
   auto seg_advance = [&]() __attribute__((always_inline)) {
     const int k1 = seg_next.k0 + kBK;
     const bool shared = seg_next.e < 0;
@@ -485,10 +553,19 @@ __global__ __launch_bounds__(kGemmThreads, Cfg::MINB) void gemm_nt_kernel(const 
       }
     } else {
       if constexpr (AL == ALoad::kSegmented) {
-        const __amdgpu_buffer_rsrc_t r = make_rsrc((const void*)seg_bptr);
+        const __amdgpu_buffer_rsrc_t r = make_rsrc((const void*)(st.e < 0 ? seg_sptr : seg_bptr));
         buf_dma16(live ? r : rs_none, b_off[d - LD_A], (uint32_t)k0 * 2, dst + b_dma_off + (d - LD_A) * 1024);
       } else if constexpr (AL == ALoad::kConcat) {
         const __amdgpu_buffer_rsrc_t r = make_rsrc((const void*)(k0 >= p.k_split ? b2_base : b_base));
+        buf_dma16(live ? r : rs_none, b_off[d - LD_A], (uint32_t)k0 * 2, dst + b_dma_off + (d - LD_A) * 1024);
+      } else if constexpr (kSharedB) {
+        const __amdgpu_buffer_rsrc_t r = make_rsrc((const void*)(k0 < p.k_split ? b2_base : b_base));
+        buf_dma16(live ? r : rs_none, b_off[d - LD_A], (uint32_t)k0 * 2, dst + b_dma_off + (d - LD_A) * 1024);
+      } else if constexpr (kGuTiles) {
+        // The instruction's rows start at wave * BN/4 + 8 j (a multiple of 8; split is a
+        // multiple of 128, so all eight rows lie on one side of it).
+        const int row0 = wave * (kBN / 4) + (d - LD_A) * ROWS_PER_DMA;
+        const __amdgpu_buffer_rsrc_t r = make_rsrc((const void*)(row0 >= gu.split ? gu.hi : gu.lo));
         buf_dma16(live ? r : rs_none, b_off[d - LD_A], (uint32_t)k0 * 2, dst + b_dma_off + (d - LD_A) * 1024);
       } else {
         buf_dma16(live ? rs_b : rs_none, b_off[d - LD_A], (uint32_t)k0 * 2, dst + b_dma_off + (d - LD_A) * 1024);
@@ -853,7 +930,7 @@ __global__ __launch_bounds__(kGemmThreads, Cfg::MINB) void gemm_nt_kernel(const 
 #pragma unroll
       for (int ni = 0; ni < NI; ++ni) {
         const int n = n0 + wn * WN + ni * 16 + 4 * q4;
-        bias4[ni] = n < p.N ? *reinterpret_cast<const float4*>(p.bias + n) : make_float4(0.f, 0.f, 0.f, 0.f);
+        bias4[ni] = n < p.N ? load_bias4(p.bias + n, p.bias_lo, p.bias_hi) : make_float4(0.f, 0.f, 0.f, 0.f);
       }
     }
 #pragma unroll

@@ -9,7 +9,8 @@
 //                        stream in place (the block's h = h + mlp(x))
 //   cdx_grouped_gemm_fwd plain grouped GEMM over expert segments
 //   cdx_mu_guidance_fwd  mu = clamp(h @ W_mu^T + clamp(mu_param), lo, hi), the
-//                        producer of the next layer's mu operand
+//                        producer of the next layer's mu operand (the parameter is
+//                        read and clamped in the epilogue)
 //   cdx_linear_fwd       y = x @ W^T (the tied LM head)
 #include "cdx_gemm_persist.h"
 
@@ -142,10 +143,16 @@ int moe_swiglu(const uint16_t* x, int64_t T, int32_t H, int32_t Ie, int32_t E, i
   const int32_t S = has_shared ? 2 : 1;
   const int32_t n_gu = 2 * S * P;
   const int32_t k_down = S * P;
+  const int64_t blocks = (int64_t)E + (has_shared ? 1 : 0);
+  // The kernels address each weight operand with 32-bit offsets from a tile base.
+  if (blocks * 2 * P * (int64_t)H * 2 > (int64_t)UINT32_MAX)
+    return fail(CDX_EUNSUPPORTED, "%s: the gate/up weights must fit 4 GB (E=%d, P=%d, H=%d)", name, E, P, H);
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
   const int32_t mt = (int32_t)(cdiv(T, kBM) + E);
 
-  // Pass 1: gathered rows x[perm] times the expert's gate/up rows, SwiGLU epilogue.
+  // Pass 1: gathered rows x[perm] times the gate/up rows of the shared block and the
+  // token's expert block (w_gu [blocks][2][P][H]), SwiGLU epilogue; logical N rows
+  // [0, S 2P) per expert (gu_tile).
   GemmParams p1{};
   p1.a = x;
   p1.lda = H;
@@ -156,7 +163,9 @@ int moe_swiglu(const uint16_t* x, int64_t T, int32_t H, int32_t Ie, int32_t E, i
   p1.M = T;
   p1.b = w_gu;
   p1.ldb = H;
-  p1.b_estride = (int64_t)n_gu * H;
+  p1.b_estride = 0;
+  p1.gu_P = P;
+  p1.gu_shared = has_shared ? 1 : 0;
   p1.N = n_gu;
   p1.K = H;
   p1.c = inter;
@@ -177,17 +186,20 @@ int moe_swiglu(const uint16_t* x, int64_t T, int32_t H, int32_t Ie, int32_t E, i
   const int64_t cost_expert = cdiv((cdiv(T, kBM) + E - 1) * nt2, cus) * (ks_shared + ks_expert);
   const int64_t cost_segmented = cdiv(cdiv(T, kBM) * nt2, cus) * (ks_shared + ks_expert) + ks_expert;
   const bool segmented = cost_segmented < cost_expert;
+  // B: w_down [blocks][H][P]; the shared block (if any) serves K columns [0, P), the
+  // token's expert block K columns [k_split, K).
   GemmParams p2{};
   p2.a = inter;
   p2.lda = k_down;
-  p2.k_split = segmented ? (has_shared ? P : 0) : k_down;
+  p2.k_split = has_shared ? P : 0;
   p2.perm = perm;
   p2.offsets = offsets;
   p2.E = E;
   p2.M = T;
-  p2.b = w_down;
-  p2.ldb = k_down;
-  p2.b_estride = (int64_t)H * k_down;
+  p2.b = w_down + (has_shared ? (int64_t)H * P : 0);
+  p2.b2 = has_shared ? w_down : nullptr;
+  p2.ldb = P;
+  p2.b_estride = (int64_t)H * P;
   p2.N = H;
   p2.K = k_down;
   p2.c = out;
@@ -335,16 +347,17 @@ extern "C" int cdx_mu_qkv_rope_fwd(const uint16_t* x, int64_t ldx, const uint16_
 }
 
 extern "C" int cdx_mu_guidance_fwd(const uint16_t* h, int64_t T, int32_t H, const uint16_t* w,
-                                   const float* bias, float lo, float hi, uint16_t* out, void* stream) {
+                                   const uint16_t* mu, float mu_lo, float mu_hi, float lo, float hi, uint16_t* out,
+                                   void* stream) {
   using namespace cdx;
   clear_error();
   const char* name = "cdx_mu_guidance_fwd";
   if (T < 0 || H <= 0) return fail(CDX_EINVAL, "%s: bad shape T=%lld H=%d", name, (long long)T, H);
   if (H % 64 != 0) return fail(CDX_EUNSUPPORTED, "%s: H=%d must be a multiple of 64", name, H);
-  if (!(lo <= hi)) return fail(CDX_EINVAL, "%s: clamp range must satisfy lo <= hi", name);
+  if (!(lo <= hi) || !(mu_lo <= mu_hi)) return fail(CDX_EINVAL, "%s: clamp ranges must satisfy lo <= hi", name);
   if (T == 0) return CDX_OK;
-  if (!h || !w || !bias || !out) return fail(CDX_EINVAL, "%s: null pointer", name);
-  if (!aligned16(h) || !aligned16(w) || !aligned16(bias) || !aligned16(out))
+  if (!h || !w || !mu || !out) return fail(CDX_EINVAL, "%s: null pointer", name);
+  if (!aligned16(h) || !aligned16(w) || !aligned16(mu) || !aligned16(out))
     return fail(CDX_EUNSUPPORTED, "%s: pointers must be 16-byte aligned", name);
   GemmParams p{};
   p.a = h;
@@ -358,7 +371,9 @@ extern "C" int cdx_mu_guidance_fwd(const uint16_t* h, int64_t T, int32_t H, cons
   p.K = H;
   p.c = out;
   p.ldc = H;
-  p.bias = bias;
+  p.bias = mu;
+  p.bias_lo = mu_lo;
+  p.bias_hi = mu_hi;
   p.lo = lo;
   p.hi = hi;
   if (cdiv(T, kBM) > INT32_MAX) return fail(CDX_EUNSUPPORTED, "%s: T too large", name);
@@ -373,8 +388,12 @@ extern "C" int cdx_linear_fwd(const uint16_t* x, int64_t ldx, const uint16_t* w,
   const char* name = "cdx_linear_fwd";
   if (M < 0 || K <= 0 || N <= 0) return fail(CDX_EINVAL, "%s: bad shape M=%lld K=%d N=%d", name, (long long)M, K, N);
   if (K % 64 != 0) return fail(CDX_EUNSUPPORTED, "%s: K=%d must be a multiple of 64", name, K);
-  if (N % 8 != 0) return fail(CDX_EUNSUPPORTED, "%s: N=%d must be a multiple of 8", name, N);
-  if (ldx < K || ldw < K || ldo < N) return fail(CDX_EINVAL, "%s: leading dimension too small", name);
+  // Results are stored in 16-byte pieces: columns [N, round_up(N, 8)) of each output
+  // row receive values of no meaning, so ldo must leave room for them.
+  const int64_t n8 = ((int64_t)N + 7) / 8 * 8;
+  if (ldx < K || ldw < K || ldo < n8)
+    return fail(CDX_EINVAL, "%s: leading dimension too small (ldo must be >= round_up(N, 8) = %lld)", name,
+                (long long)n8);
   if (ldx % 8 || ldw % 8 || ldo % 8)
     return fail(CDX_EUNSUPPORTED, "%s: leading dimensions must be multiples of 8", name);
   if (M == 0) return CDX_OK;

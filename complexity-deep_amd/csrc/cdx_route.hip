@@ -22,6 +22,9 @@
 // The count table is the only scratch: caller workspace (cdx_route_plan) or a
 // library-owned device array (cdx_route_plan_noalloc).  Nothing needs zeroing: the
 // count launch writes every entry the scatter launch reads.
+// cdx_route_plans runs L plans over the same ids, one per expert map (a model's
+// layers each route through their own map), in the same two launches: the plan
+// index is blockIdx.y, and every output and the count table gain a leading [L] axis.
 #include <mutex>
 
 #include "cdx_common.h"
@@ -34,6 +37,12 @@ constexpr int kChunks = kRound / kWave;      // 16 chunks of 64
 constexpr int kMaxE = 64;
 constexpr int kMaxBlocks = 256;
 constexpr int kScratchInts = kMaxBlocks * kMaxE;  // 64 KB: the largest count table
+// Plans per launch of cdx_route_plans (blockIdx.y); the maps travel in the kernel
+// arguments (1 KB), so that the host never copies a pointer table to the device.
+constexpr int kMaxMaps = 128;
+struct MapSet {
+  const int64_t* m[kMaxMaps];
+};
 
 // Tokens per block: a multiple of kRound such that the block count is <= kMaxBlocks.
 inline int64_t tokens_per_block(int64_t T) {
@@ -56,12 +65,16 @@ __device__ __forceinline__ int lookup_expert(const int64_t* ids, const int64_t* 
   return (int)e;
 }
 
-__global__ __launch_bounds__(256) void route_count_kernel(const int64_t* __restrict__ ids,
-                                                          const int64_t* __restrict__ map, int64_t V, int E,
-                                                          int64_t T, int64_t tpb,
+// Plan y = blockIdx.y routes through maps.m[y] and writes expert_id[y T ..] and its
+// count table rows [y nblk ..].
+__global__ __launch_bounds__(256) void route_count_kernel(const int64_t* __restrict__ ids, const MapSet maps,
+                                                          int64_t V, int E, int64_t T, int64_t tpb,
                                                           int32_t* __restrict__ expert_id,
                                                           int32_t* __restrict__ blk_counts) {
   __shared__ int cnt[kMaxE];
+  const int64_t* map = maps.m[blockIdx.y];
+  expert_id += (int64_t)blockIdx.y * T;
+  blk_counts += (int64_t)blockIdx.y * gridDim.x * E;
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
   if (threadIdx.x < E) cnt[threadIdx.x] = 0;
@@ -102,6 +115,14 @@ __global__ __launch_bounds__(256) void route_scatter_kernel(const int32_t* __res
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
   const int blk = blockIdx.x;
+  // Plan blockIdx.y: its rows of every output and of the count table.
+  const int64_t y = blockIdx.y;
+  expert_id += y * T;
+  perm += y * T;
+  inv_perm += y * T;
+  counts += y * E;
+  offsets += y * (E + 1);
+  blk_counts += y * nblk * E;
 
   // Per expert: all blocks' tokens (total) and those of blocks before this one.
   for (int x = wave; x < E; x += 4) {
@@ -181,18 +202,22 @@ __global__ __launch_bounds__(256) void route_scatter_kernel(const int32_t* __res
   }
 }
 
-// Both launches of a plan; blk_counts holds nblk * E ints.
-int route_plan_launch(const int64_t* ids, int64_t T, const int64_t* map, int64_t V, int32_t E, int32_t* expert_id,
-                      int32_t* perm, int32_t* inv_perm, int32_t* counts, int32_t* offsets, int32_t* blk_counts,
-                      hipStream_t s, const char* name) {
+// Both launches of L <= kMaxMaps plans over the same ids (plan y through maps[y],
+// outputs at row y of each [L, ...] array); blk_counts holds L * nblk * E ints.
+int route_plan_launch(const int64_t* ids, int64_t T, const int64_t* const* maps, int32_t L, int64_t V, int32_t E,
+                      int32_t* expert_id, int32_t* perm, int32_t* inv_perm, int32_t* counts, int32_t* offsets,
+                      int32_t* blk_counts, hipStream_t s, const char* name) {
   const int64_t tpb = tokens_per_block(T);
   const int nblk = (int)((T + tpb - 1) / tpb);
+  MapSet ms{};
+  for (int y = 0; y < L; ++y) ms.m[y] = maps[y];
   if (nblk > 0) {
-    route_count_kernel<<<dim3((unsigned)nblk), dim3(256), 0, s>>>(ids, map, V, E, T, tpb, expert_id, blk_counts);
+    route_count_kernel<<<dim3((unsigned)nblk, (unsigned)L), dim3(256), 0, s>>>(ids, ms, V, E, T, tpb, expert_id,
+                                                                                blk_counts);
     if (int rc = check_launch(name)) return rc;
   }
-  // At least one block: with T == 0 it writes the zero counts and offsets.
-  route_scatter_kernel<<<dim3((unsigned)(nblk > 0 ? nblk : 1)), dim3(256), 0, s>>>(
+  // At least one block per plan: with T == 0 it writes the zero counts and offsets.
+  route_scatter_kernel<<<dim3((unsigned)(nblk > 0 ? nblk : 1), (unsigned)L), dim3(256), 0, s>>>(
       expert_id, E, T, tpb, nblk, blk_counts, perm, inv_perm, counts, offsets);
   return check_launch(name);
 }
@@ -242,6 +267,43 @@ __global__ __launch_bounds__(256) void permute_rows_kernel(const uint4* __restri
   }
 }
 
+// Rows whose length or base is not a multiple of 16 bytes (a token matrix of any
+// width, as tokens[sorted_indices] takes): one wave per row moving W-byte words, W the
+// widest power of two below 16 that divides the row length and both bases.
+template <bool GATHER, typename W>
+__global__ __launch_bounds__(256) void permute_rows_narrow_kernel(const W* __restrict__ in,
+                                                                  const int32_t* __restrict__ perm, int64_t T,
+                                                                  int64_t words, W* __restrict__ out) {
+  const int lane = threadIdx.x & 63;
+  const int64_t i = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (i >= T) return;
+  const int64_t p = perm[i];
+  if (p < 0 || p >= T) return;
+  const W* src = in + (GATHER ? p : i) * words;
+  W* dst = out + (GATHER ? i : p) * words;
+  for (int64_t v = lane; v < words; v += kWave) dst[v] = src[v];
+}
+
+template <bool GATHER>
+int permute_narrow_launch(const void* in, const int32_t* perm, int64_t T, int64_t row_bytes, void* out,
+                          hipStream_t s) {
+  const uintptr_t a = (uintptr_t)in | (uintptr_t)out | (uintptr_t)row_bytes;
+  const dim3 grid((unsigned)((T + 3) / 4)), block(256);
+  if (a % 8 == 0)
+    permute_rows_narrow_kernel<GATHER, uint64_t><<<grid, block, 0, s>>>(
+        static_cast<const uint64_t*>(in), perm, T, row_bytes / 8, static_cast<uint64_t*>(out));
+  else if (a % 4 == 0)
+    permute_rows_narrow_kernel<GATHER, uint32_t><<<grid, block, 0, s>>>(
+        static_cast<const uint32_t*>(in), perm, T, row_bytes / 4, static_cast<uint32_t*>(out));
+  else if (a % 2 == 0)
+    permute_rows_narrow_kernel<GATHER, uint16_t><<<grid, block, 0, s>>>(
+        static_cast<const uint16_t*>(in), perm, T, row_bytes / 2, static_cast<uint16_t*>(out));
+  else
+    permute_rows_narrow_kernel<GATHER, uint8_t><<<grid, block, 0, s>>>(
+        static_cast<const uint8_t*>(in), perm, T, row_bytes, static_cast<uint8_t*>(out));
+  return CDX_OK;
+}
+
 }  // namespace
 }  // namespace cdx
 
@@ -262,8 +324,44 @@ extern "C" int cdx_route_plan(const int64_t* ids, int64_t T, const int64_t* map,
   const size_t need = cdx_route_workspace_bytes(T, E);
   if (need > 0 && (workspace == nullptr || workspace_bytes < need))
     return fail(CDX_EWORKSPACE, "%s: workspace needs %zu bytes, got %zu", name, need, workspace_bytes);
-  return route_plan_launch(ids, T, map, V, E, expert_id, perm, inv_perm, counts, offsets,
+  return route_plan_launch(ids, T, &map, 1, V, E, expert_id, perm, inv_perm, counts, offsets,
                            static_cast<int32_t*>(workspace), reinterpret_cast<hipStream_t>(stream), name);
+}
+
+extern "C" size_t cdx_route_plans_workspace_bytes(int64_t T, int32_t E, int32_t L) {
+  if (L <= 0) return 0;
+  return cdx_route_workspace_bytes(T, E) * (size_t)L;
+}
+
+extern "C" int cdx_route_plans(const int64_t* ids, int64_t T, const int64_t* const* maps, int32_t L, int64_t V,
+                               int32_t E, int32_t* expert_id, int32_t* perm, int32_t* inv_perm, int32_t* counts,
+                               int32_t* offsets, void* workspace, size_t workspace_bytes, void* stream) {
+  using namespace cdx;
+  clear_error();
+  const char* name = "cdx_route_plans";
+  if (L < 0) return fail(CDX_EINVAL, "%s: L=%d must be >= 0", name, L);
+  if (L == 0) return CDX_OK;
+  if (!maps) return fail(CDX_EINVAL, "%s: null map table", name);
+  for (int32_t y = 0; y < L; ++y)
+    if (!maps[y]) return fail(CDX_EINVAL, "%s: map %d is NULL", name, y);
+  if (int rc = route_plan_check(ids, T, maps[0], V, E, expert_id, perm, inv_perm, counts, offsets, name)) return rc;
+  if ((int64_t)L * T > INT32_MAX)
+    return fail(CDX_EUNSUPPORTED, "%s: L * T = %lld exceeds 2^31 - 1", name, (long long)L * T);
+  const size_t need = cdx_route_plans_workspace_bytes(T, E, L);
+  if (need > 0 && (workspace == nullptr || workspace_bytes < need))
+    return fail(CDX_EWORKSPACE, "%s: workspace needs %zu bytes, got %zu", name, need, workspace_bytes);
+  const size_t per = cdx_route_workspace_bytes(T, E) / sizeof(int32_t);
+  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  // Launches of at most kMaxMaps plans each (the map table travels in the arguments).
+  for (int32_t y0 = 0; y0 < L; y0 += kMaxMaps) {
+    const int32_t n = L - y0 < kMaxMaps ? L - y0 : kMaxMaps;
+    const int64_t r = (int64_t)y0;
+    if (int rc = route_plan_launch(ids, T, maps + y0, n, V, E, expert_id + r * T, perm + r * T, inv_perm + r * T,
+                                   counts + r * E, offsets + r * (E + 1),
+                                   static_cast<int32_t*>(workspace) + r * per, s, name))
+      return rc;
+  }
+  return CDX_OK;
 }
 
 // ---- allocation-free variant --------------------------------------------------
@@ -317,7 +415,7 @@ extern "C" int cdx_route_plan_noalloc(const int64_t* ids, int64_t T, const int64
                 sizeof(scratch));
   int32_t* table = nullptr;
   if (int rc = scratch_on_current_device(&table, name)) return rc;
-  return route_plan_launch(ids, T, map, V, E, expert_id, perm, inv_perm, counts, offsets, table,
+  return route_plan_launch(ids, T, &map, 1, V, E, expert_id, perm, inv_perm, counts, offsets, table,
                            reinterpret_cast<hipStream_t>(stream), name);
 }
 
@@ -326,11 +424,15 @@ static int permute_common(const void* in, const int32_t* perm, int64_t T, int64_
   using namespace cdx;
   clear_error();
   if (T < 0 || row_bytes <= 0) return fail(CDX_EINVAL, "%s: bad shape", name);
-  if (row_bytes % 16 != 0) return fail(CDX_EUNSUPPORTED, "%s: row_bytes=%lld must be a multiple of 16", name, (long long)row_bytes);
+  if (T > INT32_MAX) return fail(CDX_EUNSUPPORTED, "%s: T=%lld exceeds 2^31 - 1", name, (long long)T);
   if (T == 0) return CDX_OK;
   if (!in || !perm || !out) return fail(CDX_EINVAL, "%s: null pointer", name);
-  if (!aligned16(in) || !aligned16(out)) return fail(CDX_EUNSUPPORTED, "%s: pointers must be 16-byte aligned", name);
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  if (row_bytes % 16 != 0 || !aligned16(in) || !aligned16(out)) {
+    const int rc = gather ? permute_narrow_launch<true>(in, perm, T, row_bytes, out, s)
+                          : permute_narrow_launch<false>(in, perm, T, row_bytes, out, s);
+    return rc ? rc : check_launch(name);
+  }
   const dim3 grid((unsigned)((T + 3) / 4));
   if (gather)
     permute_rows_kernel<true><<<grid, dim3(256), 0, s>>>(static_cast<const uint4*>(in), perm, T, row_bytes / 16, static_cast<uint4*>(out));

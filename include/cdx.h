@@ -95,6 +95,23 @@ int cdx_route_plan(const int64_t* ids_dev, int64_t T, const int64_t* map_dev, in
                    void* workspace_dev, size_t workspace_bytes, void* stream);
 
 /*
+ * L routing plans over the same ids, plan y through its own map maps[y] (`maps` is a host array
+ * of L device pointers, none NULL, all of V entries), in two launches for all of them.
+ * Outputs gain a leading [L] axis: expert_id / perm / inv_perm [L][T], counts [L][E],
+ * offsets [L][E+1]; row y is exactly cdx_route_plan(ids, T, maps[y], ...).  The
+ * workspace holds one count table per plan (cdx_route_plans_workspace_bytes).
+ * L * T must stay below 2^31.  L == 0 does nothing.
+ *
+ * Replaces: core/token_routed_mlp.py:149-150 called from each layer's MLP
+ * (core/layer.py:180): every layer looks its tokens up in its own token_to_expert.
+ */
+size_t cdx_route_plans_workspace_bytes(int64_t T, int32_t E, int32_t L);
+int cdx_route_plans(const int64_t* ids_dev, int64_t T, const int64_t* const* maps, int32_t L,
+                    int64_t V, int32_t E, int32_t* expert_id_dev, int32_t* perm_dev,
+                    int32_t* inv_perm_dev, int32_t* counts_dev, int32_t* offsets_dev,
+                    void* workspace_dev, size_t workspace_bytes, void* stream);
+
+/*
  * cdx_route_plan without a workspace argument and without any allocation: the
  * per-block count table lives in a library-owned device array of
  * cdx_route_noalloc_scratch_bytes() bytes (64 KB: 256 blocks x 64 experts of int32),
@@ -116,9 +133,11 @@ int cdx_route_plan_noalloc(const int64_t* ids_dev, int64_t T, const int64_t* map
                            void* stream);
 
 /*
- * Row gather / scatter by a permutation (rows of `row_bytes` bytes, a multiple of 16):
+ * Row gather / scatter by a permutation (rows of `row_bytes` bytes, any length and
+ * alignment; rows that are 16-byte multiples at 16-byte aligned bases take the wide path):
  *   permute:    out[i]       = in[perm[i]]
  *   unpermute:  out[perm[i]] = in[i]
+ * An entry of perm outside [0, T) moves nothing.  T <= 2^31 - 1.
  * Replaces: cuda/triton_token_routed.py:55 (tokens[sorted_indices]) and
  * :385-386 (output[sorted_indices] = sorted_output); core/token_routed_mlp.py:170,174.
  */
@@ -130,17 +149,19 @@ int cdx_unpermute_rows(const void* in_dev, const int32_t* perm_dev, int64_t T,
 /* ---- piece 1b: token-routed SwiGLU MoE ------------------------------------ */
 
 /*
- * Packed weight layouts (bf16, K-contiguous, built once by the caller):
+ * Weight operands (bf16, K-contiguous), laid out so that the module's Parameters can
+ * be views of them (strided slices, no copy):
  *   P   = round_up(Ie, 64)                  padded expert width
  *   S   = has_shared ? 2 : 1                number of SwiGLU blocks per token
- *   w_gu   [E][S*2*P][H]   gate/up rows for the shared block (if any) then the routed
- *                          block; inside a block, rows come in groups of 64:
- *                          32 gate rows (intermediate cols j..j+31) then the 32 up rows
- *                          for the same cols.  Padding rows are zero.
- *   w_down [E][H][S*P]     row n = output feature n; cols [0,P) shared down weights
- *                          (if any), then the routed expert's down weights.  Padding
- *                          cols are zero.
- *   The shared block is replicated into each expert's slice (it is 1/S of the slice).
+ *   NB  = E + (has_shared ? 1 : 0)          weight blocks: the shared expert (if any)
+ *                                           is block 0, routed expert e block NB-E+e
+ *   w_gu   [NB][2][P][H]   w_gu[b][0][i] = gate weights of unit i (row i of the
+ *                          nn.Linear weight, column i of gate_proj_w[e]),
+ *                          w_gu[b][1][i] = the up weights of unit i.
+ *   w_down [NB][H][P]      w_down[b][n][i] = weight from unit i to output feature n
+ *                          (down_proj_w[e][i][n], the shared nn.Linear's [n][i]).
+ *   Units i in [Ie, P) are padding and must be zero.  Each block is stored once.
+ *   ((E + 1) * 2 * P * H * 2 bytes must stay below 4 GB.)
  *
  * Computes, for every token t with e = expert_id[t]:
  *   a_s = silu(x_t Wsg^T) * (x_t Wsu^T)          (if has_shared)
@@ -257,17 +278,19 @@ int cdx_mu_qkv_rope_fwd(const uint16_t* x_dev, int64_t ldx, const uint16_t* mu_d
 
 /*
  * mu guidance, the producer of the next layer's mu operand:
- *   out[t, n] = clamp(sum_k h[t, k] w[n, k] + bias[n], lo, hi)
- * h [T, H] bf16, w [H, H] bf16 (nn.Linear layout, [out, in]), bias [H] fp32, out [T, H]
- * bf16; fp32 accumulation, one rounding.  The model passes bias = clamp(mu_param,
- * mu_min, mu_max) and (lo, hi) = (-2, 2), its clamp of mu between layers; the module
- * API passes (lo, hi) = (-inf, +inf).  H must be a multiple of 64.
+ *   out[t, n] = clamp(sum_k h[t, k] w[n, k] + clamp(mu[n], mu_lo, mu_hi), lo, hi)
+ * h [T, H] bf16, w [H, H] bf16 (nn.Linear layout, [out, in]), mu [H] bf16 (the
+ * MuGuidance parameter, read on every call), out [T, H] bf16; fp32 accumulation, one
+ * rounding.  (mu_lo, mu_hi) are the module's (mu_min, mu_max); the model passes
+ * (lo, hi) = (-2, 2), its clamp of mu between layers, the module API (-inf, +inf).
+ * H must be a multiple of 64.
  *
  * Replaces: core/layer.py:54-61 (MuGuidance.forward: clamp(mu) + mu_proj(h)) and
  * models/modeling.py:199-200 (mu_prev = clamp(mu, -2, 2)).
  */
 int cdx_mu_guidance_fwd(const uint16_t* h_dev, int64_t T, int32_t H, const uint16_t* w_dev,
-                        const float* bias_dev, float lo, float hi, uint16_t* out_dev, void* stream);
+                        const uint16_t* mu_dev, float mu_lo, float mu_hi, float lo, float hi,
+                        uint16_t* out_dev, void* stream);
 
 /*
  * Causal GQA attention over the fused projection's outputs:
@@ -317,8 +340,10 @@ int cdx_embedding_fwd(const int64_t* ids_dev, int64_t T, const uint16_t* table_d
 /*
  * out[M, N] = x[M, K] @ w[N, K]^T, bf16 in and out, fp32 accumulation, one rounding:
  * nn.Linear without bias with its weight as stored ([out, in]).  The model calls it
- * for the tied LM head, w = the embedding table.  K % 64 == 0, N % 8 == 0, leading
- * dimensions multiples of 8, pointers 16-byte aligned.
+ * for the tied LM head, w = the embedding table.  K % 64 == 0; any N >= 1, with
+ * ldo >= round_up(N, 8): the columns [N, round_up(N, 8)) of every output row are
+ * written with values of no meaning.  Leading dimensions multiples of 8, pointers
+ * 16-byte aligned.
  *
  * Replaces: models/modeling.py:101-103,206 (lm_head, weight tied to embed_tokens).
  */

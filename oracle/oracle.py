@@ -33,7 +33,7 @@ import ctypes
 import math
 import subprocess
 from pathlib import Path
-from typing import Dict, Optional
+from typing import Dict, Optional, Tuple
 
 import numpy as np
 import torch
@@ -275,6 +275,56 @@ def causal_attention(q, k, v):
     return o.transpose(1, 2).reshape(B, S, nq * D)
 
 
+def attention_half(sd: Dict[str, torch.Tensor], cfg: dict, i: int, h: torch.Tensor,
+                   mu_prev: Optional[torch.Tensor]) -> torch.Tensor:
+    """First half of decoder block i in fp32: h + attention(input_layernorm(h), mu_prev);
+    core/layer.py:165-174."""
+    p = f"layers.{i}."
+    sd = {k: _f32(v) for k, v in sd.items() if k.startswith(p)}
+    h = _f32(h)
+    n = rms_norm(h, sd[p + "input_layernorm.weight"], cfg.get("rms_norm_eps", 1e-6))
+    return h + attention(n, None if mu_prev is None else _f32(mu_prev), sd, p + "self_attn.", cfg)
+
+
+def mlp_half(sd: Dict[str, torch.Tensor], cfg: dict, i: int, h: torch.Tensor, ids: torch.Tensor) -> torch.Tensor:
+    """Second half of decoder block i in fp32: h + mlp(post_attention_layernorm(h));
+    core/layer.py:176-183."""
+    p = f"layers.{i}."
+    sd = {k: _f32(v) for k, v in sd.items() if k.startswith(p)}
+    ids = torch.as_tensor(ids).to(torch.int64)
+    h = _f32(h)
+    n = rms_norm(h, sd[p + "post_attention_layernorm.weight"], cfg.get("rms_norm_eps", 1e-6))
+    mp = p + "mlp."
+    if cfg.get("use_token_routed_mlp", True):
+        shared = cfg.get("shared_expert", True)
+        m = token_routed_mlp(n, ids, sd[mp + "token_to_expert"].to(torch.int64).numpy(),
+                             sd[mp + "gate_proj_w"], sd[mp + "up_proj_w"], sd[mp + "down_proj_w"],
+                             sd[mp + "shared_gate.weight"] if shared else None,
+                             sd[mp + "shared_up.weight"] if shared else None,
+                             sd[mp + "shared_down.weight"] if shared else None)
+    else:
+        m = swiglu_rows(n, sd[mp + "gate_proj.weight"].t(), sd[mp + "up_proj.weight"].t(),
+                        sd[mp + "down_proj.weight"].t())
+    return h + m
+
+
+def mu_out(sd: Dict[str, torch.Tensor], i: int, h: torch.Tensor) -> torch.Tensor:
+    """mu of decoder block i from its output h, clamped to [-2, 2] as the model does
+    between layers; core/layer.py:54-61, models/modeling.py:199-200."""
+    p = f"layers.{i}.mu_guidance."
+    mu = torch.clamp(_f32(sd[p + "mu"]), 0.0, 2.0) + _f32(h) @ _f32(sd[p + "mu_proj.weight"]).t()
+    return torch.clamp(mu, -2.0, 2.0)
+
+
+def layer(sd: Dict[str, torch.Tensor], cfg: dict, i: int, h: torch.Tensor, mu_prev: Optional[torch.Tensor],
+          ids: torch.Tensor) -> Tuple[torch.Tensor, Optional[torch.Tensor]]:
+    """Decoder block i in fp32: (h_out, mu clamped to [-2, 2] or None) from the block
+    input h and the previous mu; core/layer.py:141-190 with the model's clamp of
+    models/modeling.py:199-200."""
+    h = mlp_half(sd, cfg, i, attention_half(sd, cfg, i, h, mu_prev), ids)
+    return h, (mu_out(sd, i, h) if cfg.get("use_mu_guidance", True) else None)
+
+
 def forward(sd: Dict[str, torch.Tensor], cfg: dict, input_ids: torch.Tensor) -> torch.Tensor:
     """Full ComplexityModel forward in fp32 -> logits [B, S, V]; modeling.py:176-206.
 
@@ -290,25 +340,7 @@ def forward(sd: Dict[str, torch.Tensor], cfg: dict, input_ids: torch.Tensor) -> 
     h = sd["embed_tokens.weight"][ids]
     mu_prev = sd["mu_init"].expand(B, S, H) if use_mu else None
     for i in range(cfg["num_hidden_layers"]):
-        p = f"layers.{i}."
-        n = rms_norm(h, sd[p + "input_layernorm.weight"], eps)
-        h = h + attention(n, mu_prev, sd, p + "self_attn.", cfg)
-        n = rms_norm(h, sd[p + "post_attention_layernorm.weight"], eps)
-        mp = p + "mlp."
-        if cfg.get("use_token_routed_mlp", True):
-            shared = cfg.get("shared_expert", True)
-            m = token_routed_mlp(n, ids, sd[mp + "token_to_expert"].to(torch.int64).numpy(),
-                                 sd[mp + "gate_proj_w"], sd[mp + "up_proj_w"], sd[mp + "down_proj_w"],
-                                 sd[mp + "shared_gate.weight"] if shared else None,
-                                 sd[mp + "shared_up.weight"] if shared else None,
-                                 sd[mp + "shared_down.weight"] if shared else None)
-        else:
-            m = swiglu_rows(n, sd[mp + "gate_proj.weight"].t(), sd[mp + "up_proj.weight"].t(),
-                            sd[mp + "down_proj.weight"].t())
-        h = h + m
-        if use_mu:
-            mu = torch.clamp(sd[p + "mu_guidance.mu"], 0.0, 2.0) + h @ sd[p + "mu_guidance.mu_proj.weight"].t()
-            mu_prev = torch.clamp(mu, -2.0, 2.0)
+        h, mu_prev = layer(sd, cfg, i, h, mu_prev, ids)
     h = rms_norm(h, sd["norm.weight"], eps)
     lm = sd["lm_head.weight"] if "lm_head.weight" in sd else sd["embed_tokens.weight"]
     return h @ lm.t()

@@ -78,8 +78,28 @@ def test_route_validation(lib):
     assert lib.cdx_route_plan(16, 2048, 16, 5, 4, 16, 16, 16, 16, 16, 16, 8, None) == CDX_EWORKSPACE
     assert lib.cdx_route_plan(16, -1, 16, 5, 4, 16, 16, 16, 16, 16, 16, 0, None) == CDX_EINVAL
     assert lib.cdx_route_plan(None, 10, 16, 5, 4, 16, 16, 16, 16, 16, 16, 1 << 20, None) == CDX_EINVAL
-    assert lib.cdx_permute_rows(16, 16, 4, 24, 16, None) == CDX_EUNSUPPORTED
+    assert lib.cdx_permute_rows(16, 16, 1 << 31, 24, 16, None) == CDX_EUNSUPPORTED  # T >= 2^31
+    assert lib.cdx_permute_rows(16, 16, 4, 0, 16, None) == CDX_EINVAL
+    assert lib.cdx_permute_rows(None, 16, 4, 6, 16, None) == CDX_EINVAL
     assert lib.cdx_unpermute_rows(None, None, 0, 32, None, None) == 0
+
+
+def test_route_plans_validation(lib):
+    # One count table per plan.
+    assert lib.cdx_route_plans_workspace_bytes(1025, 8, 24) == 24 * 2 * 8 * 4
+    assert lib.cdx_route_plans_workspace_bytes(1025, 8, 0) == 0
+    maps = (ctypes.c_void_p * 2)(16, 16)
+    table = ctypes.cast(maps, ctypes.c_void_p)
+    assert lib.cdx_route_plans(16, 10, table, -1, 5, 4, 16, 16, 16, 16, 16, 16, 1 << 20, None) == CDX_EINVAL
+    assert lib.cdx_route_plans(16, 10, table, 0, 5, 4, 16, 16, 16, 16, 16, 16, 1 << 20, None) == 0  # no plans
+    assert lib.cdx_route_plans(16, 10, None, 2, 5, 4, 16, 16, 16, 16, 16, 16, 1 << 20, None) == CDX_EINVAL
+    nulls = ctypes.cast((ctypes.c_void_p * 2)(16, None), ctypes.c_void_p)
+    assert lib.cdx_route_plans(16, 10, nulls, 2, 5, 4, 16, 16, 16, 16, 16, 16, 1 << 20, None) == CDX_EINVAL
+    assert b"map 1 is NULL" in lib.cdx_last_error()
+    assert lib.cdx_route_plans(16, 10, table, 2, 5, 65, 16, 16, 16, 16, 16, 16, 1 << 20, None) == CDX_EUNSUPPORTED
+    assert lib.cdx_route_plans(16, 2048, table, 2, 5, 4, 16, 16, 16, 16, 16, 16, 16, None) == CDX_EWORKSPACE
+    assert lib.cdx_route_plans(16, 1 << 30, table, 2, 5, 4, 16, 16, 16, 16, 16, 16, 1 << 30, None) == \
+        CDX_EUNSUPPORTED  # L * T >= 2^31
 
 
 def test_gemm_validation(lib):
@@ -93,6 +113,11 @@ def test_gemm_validation(lib):
     assert lib.cdx_moe_swiglu_fwd(None, 0, 64, 64, 4, 1, None, None, None, None, None, None, None) == 0
     assert lib.cdx_grouped_gemm_fwd(16, 8, 48, 64, 4, 16, 16, 16, None) == CDX_EUNSUPPORTED
     assert b"multiple of 64" in lib.cdx_last_error()
+    # gate/up operand beyond 4 GB: (64 + 1) * 2 * 8192 * 8192 * 2 bytes
+    assert lib.cdx_moe_swiglu_fwd(16, 8, 8192, 8192, 64, 1, 16, 16, 16, 16, 16, 16, None) == CDX_EUNSUPPORTED
+    assert lib.cdx_mu_guidance_fwd(16, 8, 64, 16, 16, 2.0, 0.0, -2.0, 2.0, 16, None) == CDX_EINVAL  # mu_lo > mu_hi
+    assert lib.cdx_mu_guidance_fwd(16, 8, 64, 16, None, 0.0, 2.0, -2.0, 2.0, 16, None) == CDX_EINVAL  # no mu
+    assert lib.cdx_linear_fwd(16, 64, 16, 64, 8, 64, 30, 16, 30, None) == CDX_EINVAL  # ldo < round_up(N, 8)
 
 
 def test_cpu_tensors_raise():

@@ -65,9 +65,9 @@ def test_persistent_mu_guidance_many_tiles(cdx):
     g = torch.Generator().manual_seed(12)
     h = torch.randn(T, H, generator=g).to(bf16).cuda()
     w = (torch.randn(H, H, generator=g) / H ** 0.5).to(bf16).cuda()
-    bias = torch.linspace(0.0, 2.0, H).cuda()
-    out = mu_guidance(h, w, bias, -2.0, 2.0)
-    ref = torch.clamp(bias + h.float() @ w.float().t(), -2.0, 2.0)
+    bias = torch.linspace(0.0, 2.0, H).to(bf16).cuda()
+    out = mu_guidance(h, w, bias, 0.0, 2.0, -2.0, 2.0)
+    ref = torch.clamp(bias.float() + h.float() @ w.float().t(), -2.0, 2.0)
     assert_close_bf16(out, ref, "mu_guidance")
 
 
@@ -106,8 +106,8 @@ def test_tile_forms_agree_bit_for_bit(cdx, K, N):
         assert torch.equal(part, fq[:, :rows]), f"mu_qkv rows={rows}"
     if N == K:
         wm = (torch.randn(N, K, generator=g) * 0.02).to(bf16).cuda()
-        bias = torch.linspace(0.0, 2.0, N, device="cuda")
-        fm = mu_guidance(x, wm, bias, -2.0, 2.0)
+        bias = torch.linspace(0.0, 2.0, N, device="cuda").to(bf16)
+        fm = mu_guidance(x, wm, bias, 0.0, 2.0, -2.0, 2.0)
         for rows in (256, nar, mid):
-            assert torch.equal(mu_guidance(x[:rows].contiguous(), wm, bias, -2.0, 2.0), fm[:rows]), \
+            assert torch.equal(mu_guidance(x[:rows].contiguous(), wm, bias, 0.0, 2.0, -2.0, 2.0), fm[:rows]), \
                 f"mu_guidance rows={rows}"

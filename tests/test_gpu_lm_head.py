@@ -65,8 +65,45 @@ def test_linear_matches_fp32(cdx, M, K, N):
     assert_close_bf16(out, ref, f"linear {M}x{K}x{N}")
 
 
+@pytest.mark.parametrize("M,K,N", [(77, 128, 30), (300, 64, 1001), (1, 64, 1), (2, 256, 32003)])
+def test_linear_any_out_features(cdx, M, K, N):
+    """N not a multiple of 8 runs on the kernel too (the model's head for any
+    vocabulary): a view of the first N columns of a padded buffer, whose leading
+    dimensions still merge."""
+    from complexity_deep.linear import linear
+    print(f"linear odd N M={M} K={K} N={N}", flush=True)
+    g = torch.Generator().manual_seed(M * 7 + N)
+    x = torch.randn(2, M, K, generator=g).to(bf16)
+    w = (torch.randn(N, K, generator=g) * 0.05).to(bf16)
+    out = linear(x.cuda(), w.cuda())
+    torch.cuda.synchronize()
+    assert out.shape == (2, M, N)
+    assert_close_bf16(out.view(-1, N), x.float().view(-1, K) @ w.float().t(), f"linear {M}x{K}x{N}")
+
+
 def test_linear_rejects_unsupported_shapes(cdx):
-    from complexity_deep.linear import linear, linear_supported
-    assert not linear_supported(100, 64) and not linear_supported(64, 30)
-    with pytest.raises(RuntimeError, match="multiple of 8"):
-        linear(torch.randn(4, 64, device="cuda").to(bf16), torch.randn(30, 64, device="cuda").to(bf16))
+    from complexity_deep.linear import linear
+    with pytest.raises(ValueError, match="multiple of 64"):
+        linear(torch.randn(4, 100, device="cuda").to(bf16), torch.randn(64, 100, device="cuda").to(bf16))
+
+
+def test_model_head_odd_vocab_runs_the_kernel(cdx, monkeypatch):
+    """A vocabulary that is not a multiple of 8 takes the same kernel as any other
+    (no nn.Linear path): the head call goes through cdx_linear_fwd, and the logits
+    match the model run with the head in fp32."""
+    import complexity_deep.modeling as modeling
+    print("odd vocab model head", flush=True)
+    cfg = cdx.ComplexityConfig(vocab_size=1001, hidden_size=128, intermediate_size=256, num_hidden_layers=1,
+                               num_attention_heads=2, num_key_value_heads=1, num_experts=2)
+    torch.manual_seed(3)
+    m = cdx.ComplexityModel(cfg).to("cuda", bf16).eval()
+    calls = []
+    real = modeling.linear
+    monkeypatch.setattr(modeling, "linear", lambda *a, **k: calls.append(a[1].shape) or real(*a, **k))
+    monkeypatch.setattr(m.lm_head, "forward", lambda *a, **k: (_ for _ in ()).throw(AssertionError("nn.Linear")))
+    ids = torch.randint(0, 1001, (2, 24)).cuda()
+    with torch.no_grad():
+        logits = m(ids).logits
+    assert calls == [(1001, 128)]
+    assert logits.shape == (2, 24, 1001)
+    assert torch.isfinite(logits.float()).all()

@@ -4,12 +4,16 @@ The tiny golden configurations (weights drawn with the reference's seeded init, 
 same expert maps and ids) run through every hot-path kernel and are compared with
 the reference's own fp32 logits from tests/golden/model_golden.npz.  A whole
 forward stacks many bf16 roundings (embedding, attention, o_proj, mu, lm_head are
-bf16 PyTorch ops, as in the reference's bf16 run), so the bound here is the model
-level one: normwise max rel err <= 3e-2 and relative RMS <= 2e-2.
+bf16 PyTorch ops, as in the reference's bf16 run).  Against the reference's fp32
+logits, whose weights are not rounded to bf16, the bound is normwise max rel err
+<= 2e-2 and relative RMS <= 2e-2 (the weight rounding alone moves the mean abs error
+to about 1e-3 on these logits).  Against the oracle run on the model's own bf16
+weights, the whole north_star bound holds: max rel err <= 2e-2 and mean abs err
+<= 1e-3 (on top of the bf16 output rounding, tests/_metrics.py).
 
 Also checked: the unfused TransformerBlock.forward API against the oracle, the
-generate() loop with a KV cache, and that the routing plan is computed once per
-forward for layers sharing one map.
+generate() loop with a KV cache, and that one routing call per forward gives every
+layer the plan of its own map.
 """
 
 from __future__ import annotations
@@ -25,7 +29,8 @@ from _metrics import errors
 
 pytestmark = pytest.mark.gpu
 GOLDEN = Path(__file__).resolve().parent / "golden" / "model_golden.npz"
-MODEL_MAX_REL = 3e-2
+MODEL_MAX_REL = 2e-2
+MODEL_MEAN_ABS = 1e-3
 MODEL_REL_RMS = 2e-2
 
 
@@ -44,7 +49,7 @@ def _model(cdx, entry, tmap):
 
 
 @pytest.mark.parametrize("name", [m["name"] for m in _entries()[1]])
-def test_forward_matches_reference_logits(cdx, name):
+def test_forward_matches_reference_logits(cdx, oracle, name):
     print(f"model forward {name}", flush=True)
     z, meta = _entries()
     entry = next(m for m in meta if m["name"] == name)
@@ -53,8 +58,13 @@ def test_forward_matches_reference_logits(cdx, name):
     with torch.no_grad():
         logits = m(ids).logits
     e = errors(logits, torch.from_numpy(z[f"{name}/logits"]))
-    print(name, e, flush=True)
+    print(name, "vs reference fp32 logits", e, flush=True)
     assert e["max_rel"] <= MODEL_MAX_REL and e["rel_rms"] <= MODEL_REL_RMS, e
+    sd = {k: v.detach().float().cpu() for k, v in m.state_dict().items()}
+    e = errors(logits, oracle.forward(sd, entry["cfg"], ids.cpu()))
+    print(name, "vs oracle on the bf16 weights", e, flush=True)
+    assert e["max_rel"] <= MODEL_MAX_REL and e["mean_abs_kernel"] <= MODEL_MEAN_ABS \
+        and e["rel_rms"] <= MODEL_REL_RMS, e
 
 
 def test_block_api_matches_oracle(cdx, oracle):
@@ -90,6 +100,11 @@ def test_block_api_matches_oracle(cdx, oracle):
     assert e["max_rel"] <= MODEL_MAX_REL, e
 
 
+def oracle_plan(ids, tmap, E):
+    from oracle import oracle as orc
+    return orc.route_plan(ids.cpu().numpy(), tmap.cpu().numpy(), E)
+
+
 def test_generate_and_plan_reuse(cdx, monkeypatch):
     print("generate + plan reuse", flush=True)
     z, meta = _entries()
@@ -97,12 +112,19 @@ def test_generate_and_plan_reuse(cdx, monkeypatch):
     m = _model(cdx, entry, z[f"{entry['name']}/map"])
     import complexity_deep.modeling as modeling
     calls = []
-    real = modeling.route_plan
-    monkeypatch.setattr(modeling, "route_plan", lambda *a, **k: calls.append(1) or real(*a, **k))
+    real = modeling.route_plans
+    monkeypatch.setattr(modeling, "route_plans", lambda *a, **k: calls.append(len(a[1])) or real(*a, **k))
     ids = torch.from_numpy(z[f"{entry['name']}/ids"]).cuda()
     with torch.no_grad():
         m(ids)
-    assert len(calls) == 1, "layers sharing one expert map must share one routing plan"
+    routed = sum(1 for layer in m.layers if layer.use_token_routed_mlp)
+    assert calls == [routed], "one routing call per forward, one plan per routed layer"
+    plans = m.route_plans(ids)
+    for layer, plan in zip(m.layers, plans):
+        if plan is None:
+            continue
+        ref = oracle_plan(ids, layer.mlp.token_to_expert, layer.mlp.num_experts)
+        assert plan.perm.tolist() == ref["perm"].tolist() and plan.offsets.tolist() == ref["offsets"].tolist()
     out = m.generate(ids[:, :4], max_new_tokens=5, do_sample=False)
     assert out.shape == (2, 9)
     assert torch.equal(out[:, :4], ids[:, :4])

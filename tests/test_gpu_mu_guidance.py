@@ -3,8 +3,9 @@
 Reference (core/layer.py:54-61, models/modeling.py:199-200), restated in fp32 on the
 CPU: mu = clamp(mu_param, 0, 2) + h @ W_mu^T, then the model's clamp to [-2, 2].
 Checked at configuration 4's shape (16384 x 2048) with and without the outer clamp,
-at ragged token counts, with a parameter that needs its own clamp, and through the
-MuGuidance module and the block's fused path.
+at ragged token counts, with a parameter that needs its own clamp (applied by the
+kernel's epilogue), through the MuGuidance module, and after a write to the parameter
+through ``.data`` (read on every call: nothing cached).
 """
 
 from __future__ import annotations
@@ -30,9 +31,9 @@ def test_mu_guidance_matches_reference(cdx, T, H, lo, hi):
     # unit-size projections around a bias in [0, 2]: the clamp to [-2, 2] bites on about
     # a sixth of the values, and the bf16 output floor stays at the N(0, 1) level
     w = (torch.randn(H, H, generator=g) / math.sqrt(H)).to(bf16)
-    mu_param = torch.linspace(-1.0, 3.0, H)                                 # below 0 and above 2: clamped first
-    bias = torch.clamp(mu_param, 0.0, 2.0)
-    out = mu_guidance(h.cuda(), w.cuda(), bias.cuda(), lo, hi)
+    mu_param = torch.linspace(-1.0, 3.0, H).to(bf16)                        # below 0 and above 2: clamped first
+    bias = torch.clamp(mu_param.float(), 0.0, 2.0)
+    out = mu_guidance(h.cuda(), w.cuda(), mu_param.cuda(), 0.0, 2.0, lo, hi)
     ref = torch.clamp(bias + h.float() @ w.float().t(), lo, hi)
     assert_close_bf16(out, ref, "mu_guidance")
     if math.isfinite(lo):
@@ -54,3 +55,24 @@ def test_mu_guidance_module(cdx):
     ref = torch.clamp(m.mu.float().cpu(), 0, 2) + h.float() @ m.mu_proj.weight.float().cpu().t()
     assert_close_bf16(out, ref, "module (unclamped, as the reference returns it)")
     assert_close_bf16(out_clamped, torch.clamp(ref, -2, 2), "module fused clamp")
+
+
+def test_mu_guidance_follows_data_writes(cdx):
+    """A write through ``.data`` (which bumps no version counter) to either parameter
+    shows in the next call: the kernel reads both on every call."""
+    print("MuGuidance .data writes", flush=True)
+    torch.manual_seed(1)
+    m = cdx.MuGuidance(256)
+    with torch.no_grad():
+        m.mu_proj.weight.normal_(0, 0.02)
+    m = m.to(bf16).cuda()
+    h = torch.randn(3, 17, 256).to(bf16).cuda()
+    with torch.no_grad():
+        before = m(h)
+        m.mu.data.fill_(1.5)
+        m.mu_proj.weight.data.mul_(2.0)
+        after = m(h)
+    with torch.no_grad():
+        ref = 1.5 + h.float().cpu() @ m.mu_proj.weight.float().cpu().t()
+    assert not torch.equal(before, after)
+    assert_close_bf16(after, ref, "after .data writes")
