@@ -35,7 +35,9 @@ Printed: ONE JSON line on stdout.  Besides the contract keys it carries
   cpu_baseline  the fp32 CPU restatement (oracle/) timed on this host over a bounded
                 sample of the same workload, plus its agreement with the GPU logits;
                 under "readme_forward" the same for configuration 1's whole batch;
-  workloads     per extra workload: tokens/s, ms per step, roofline and kernels.
+  workloads     per extra workload: tokens/s, ms per step, roofline and kernels;
+  hbm_ceiling   measured streaming read / write / copy rates of this GPU's HBM
+                (cdx_hbm_probe), the practical ceilings of the HBM-bound kernels.
 Everything else goes to stderr.
 """
 
@@ -467,6 +469,47 @@ def cpu_baseline_readme(dev):
 
 # ---------------------------------------------------------------------------
 
+def hbm_ceilings(dev) -> dict:
+    """Measured streaming ceilings of this GPU's HBM (cdx_hbm_probe: plain read, write
+    and copy kernels, 16-byte non-temporal accesses), in TB/s of algorithmic bytes,
+    for a copy of the 1B RMSNorm's size (64 MB each way) and for buffers beyond the
+    256 MB last-level cache (512 MB).  Back-to-back launches rotating over four
+    buffers, timed by HIP events around the whole pass."""
+    import torch
+    from complexity_deep import _native as nat
+    lib = nat.lib()
+    out = {}
+    for label, mb in (("64MB", 64), ("512MB", 512)):
+        nbytes = mb << 20
+        bufs = [torch.empty(nbytes, dtype=torch.uint8, device=dev).fill_(1) for _ in range(4)]
+        dsts = [torch.empty(nbytes, dtype=torch.uint8, device=dev) for _ in range(4)]
+        sink = torch.zeros(4, dtype=torch.int32, device=dev)
+        s = torch.cuda.current_stream(dev).cuda_stream
+        res = {}
+        for mode, name, moved in ((0, "read", 1), (1, "write", 1), (2, "copy", 2)):
+            def call(i):
+                src = bufs[i % 4].data_ptr() if mode != 1 else 0
+                dst = dsts[i % 4].data_ptr() if mode != 0 else sink.data_ptr()
+                nat.check(lib.cdx_hbm_probe(mode, src, dst, nbytes, s), "cdx_hbm_probe")
+            call(0)
+            torch.cuda.synchronize()
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            iters = 20
+            e0.record()
+            for i in range(iters):
+                call(i)
+            e1.record()
+            torch.cuda.synchronize()
+            us = 1e3 * e0.elapsed_time(e1) / iters
+            res[name] = {"us": round(us, 2), "TBps": round(moved * nbytes / us / 1e6, 3),
+                         "frac_of_8TBps": round(moved * nbytes / us / 1e6 / 8.0, 4)}
+        out[label] = res
+        del bufs, dsts
+        torch.cuda.empty_cache()
+    log(f"HBM ceilings: {json.dumps(out)}")
+    return out
+
+
 def roofline_of(kernels: dict, dominant, workload: str):
     dom = next((d for d in dominant if d in kernels), None)
     if dom is None:
@@ -613,12 +656,14 @@ def main() -> int:
             del w_step
             torch.cuda.empty_cache()
 
+    ceilings = hbm_ceilings(dev) if not args.no_extras and args.workload == "1b-forward" else None
+
     rec = {"metric": METRIC, "value": round(value, 1), "unit": "tokens/s", "n_gpus": 1, "steps": args.steps,
            "warmup": args.warmup, "ms_per_step": round(ms, 4), "higher_is_better": True, "scaling": "weak",
            "vs_baseline": None, "dtype": "bf16", "data": "synthetic", "config": config,
            "roofline": roofline, "cpu_baseline": cpu,
            "kernels": kernels, "hot_path_ms_per_step": round(hot_ms, 4),
-           "workloads": workloads, "device": torch.cuda.get_device_name(dev)}
+           "workloads": workloads, "hbm_ceiling": ceilings, "device": torch.cuda.get_device_name(dev)}
     print(json.dumps(rec), flush=True)
     return 0
 

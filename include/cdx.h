@@ -350,6 +350,19 @@ int cdx_embedding_fwd(const int64_t* ids_dev, int64_t T, const uint16_t* table_d
 int cdx_linear_fwd(const uint16_t* x_dev, int64_t ldx, const uint16_t* w_dev, int64_t ldw, int64_t M, int32_t K,
                    int32_t N, uint16_t* out_dev, int64_t ldo, void* stream);
 
+/* ---- measurement ---------------------------------------------------------- */
+
+/*
+ * Streaming probe of the HBM ceilings the bandwidth-bound kernels are compared with:
+ *   mode 0  read `bytes` of in_dev (out_dev: a 4-byte sink, almost never written)
+ *   mode 1  write `bytes` to out_dev (in_dev ignored)
+ *   mode 2  copy `bytes` from in_dev to out_dev
+ * 16-byte non-temporal accesses; bytes a multiple of 16, pointers 16-byte aligned.
+ *
+ * No counterpart in the reference: it measures the hardware, for the benchmark.
+ */
+int cdx_hbm_probe(int32_t mode, const void* in_dev, void* out_dev, int64_t bytes, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -84,6 +84,14 @@ def test_route_validation(lib):
     assert lib.cdx_unpermute_rows(None, None, 0, 32, None, None) == 0
 
 
+def test_hbm_probe_validation(lib):
+    assert lib.cdx_hbm_probe(3, 16, 16, 1024, None) == CDX_EINVAL
+    assert lib.cdx_hbm_probe(0, 16, 16, 1000, None) == CDX_EINVAL  # not a multiple of 16
+    assert lib.cdx_hbm_probe(2, None, 16, 1024, None) == CDX_EINVAL
+    assert lib.cdx_hbm_probe(0, 8, 16, 1024, None) == CDX_EUNSUPPORTED  # misaligned
+    assert lib.cdx_hbm_probe(1, None, None, 0, None) == 0
+
+
 def test_route_plans_validation(lib):
     # One count table per plan.
     assert lib.cdx_route_plans_workspace_bytes(1025, 8, 24) == 24 * 2 * 8 * 4
