@@ -24,7 +24,7 @@ from .normalization import (FusedResidualRMSNorm, RMSNorm, fused_add_rmsnorm_inp
 from .rotary import RotaryEmbedding, apply_rotary_pos_emb
 from .token_routed_mlp import (RoutePlan, TokenRoutedMLP, cggr_grouped_gemm, cggr_grouped_gemm_triton,
                                fused_swiglu_simple, fused_swiglu_triton, grouped_gemm_pytorch,
-                               persistent_cggr_gemm, persistent_swiglu_cggr, route_plan, sort_tokens_by_expert,
+                               persistent_cggr_gemm, persistent_swiglu_cggr, route_plan, route_plans, sort_tokens_by_expert,
                                sort_tokens_by_expert_fast)
 
 __version__ = "1.0.0"
@@ -36,6 +36,6 @@ __all__ = [
     "fused_residual_rmsnorm", "fused_add_rmsnorm_inplace", "fused_rmsnorm", "FusedResidualRMSNorm",
     "sort_tokens_by_expert", "sort_tokens_by_expert_fast", "cggr_grouped_gemm", "cggr_grouped_gemm_triton",
     "grouped_gemm_pytorch", "persistent_cggr_gemm", "persistent_swiglu_cggr", "fused_swiglu_triton",
-    "fused_swiglu_simple", "route_plan", "RoutePlan",
+    "fused_swiglu_simple", "route_plan", "route_plans", "RoutePlan",
     "fused_mu_qkv_projection", "FusedMuQKVProjection",
 ]

@@ -18,12 +18,21 @@ int check_launch(const char* what);
 
 inline bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
-// Compute units of the current device (256 on MI355X, the fallback if the query fails).
+// Compute units of the current device (256 on MI355X, the fallback if the query fails),
+// looked up once per device: launch paths call this several times per GEMM, and a
+// small forward is paced by its host-side launch cost.
 inline int device_cu_count() {
-  int dev = 0, cus = 0;
-  if (hipGetDevice(&dev) != hipSuccess ||
-      hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0)
-    cus = 256;
+  constexpr int kMaxDev = 64;
+  static int cached[kMaxDev] = {};  // 0 = not looked up yet (benign race: same value)
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) return 256;
+  if (dev >= 0 && dev < kMaxDev) {
+    const int c = __atomic_load_n(&cached[dev], __ATOMIC_RELAXED);
+    if (c > 0) return c;
+  }
+  int cus = 0;
+  if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0) cus = 256;
+  if (dev >= 0 && dev < kMaxDev) __atomic_store_n(&cached[dev], cus, __ATOMIC_RELAXED);
   return cus;
 }
 
