@@ -99,3 +99,55 @@ def test_plan_large_token_counts(cdx, oracle, T, E):
     tmap = torch.randint(0, E, (32000,), generator=g)
     plan = cdx.route_plan(ids.cuda(), tmap.cuda(), E)
     _check(plan, oracle.route_plan(ids.numpy(), tmap.numpy(), E))
+
+
+@pytest.mark.parametrize("T,L,E,V", [(16384, 24, 8, 32000), (2048, 18, 4, 32000), (1025, 130, 8, 500),
+                                     (0, 3, 4, 100), (777, 1, 64, 1000)])
+def test_route_plans_each_map(cdx, oracle, T, L, E, V):
+    """cdx_route_plans: plan y of one call equals the oracle's plan of map y over the
+    same ids, for L maps (L = 130 crosses the 128-plans-per-launch chunk), with maps
+    that are equal, permuted, degenerate (one expert) and random."""
+    print(f"route plans T={T} L={L} E={E} V={V}", flush=True)
+    g = torch.Generator().manual_seed(T + L)
+    ids = torch.randint(-3, V + 3, (T,), generator=g)
+    base = torch.randint(0, E, (V,), generator=g)
+    maps = []
+    for y in range(L):
+        kind = y % 4
+        if kind == 0:
+            m = base.clone()
+        elif kind == 1:
+            m = (base + y) % E
+        elif kind == 2:
+            m = torch.full((V,), y % E, dtype=torch.long)
+        else:
+            m = torch.randint(0, E, (V,), generator=g)
+        maps.append(m)
+    plans = cdx.route_plans(ids.cuda(), [m.cuda() for m in maps], E)
+    assert len(plans) == L
+    for y, (plan, m) in enumerate(zip(plans, maps)):
+        _check(plan, oracle.route_plan(ids.numpy(), m.numpy(), E))
+
+
+@pytest.mark.parametrize("W,dtype,offset", [(3, torch.bfloat16, 0), (5, torch.float32, 0), (7, torch.uint8, 1),
+                                             (12, torch.int16, 1), (2048, torch.bfloat16, 1)])
+def test_permute_rows_any_width(cdx, W, dtype, offset):
+    """Rows that are not whole 16-byte vectors, or whose base is not 16-byte aligned
+    (a slice one element in), gather and scatter exactly, as tokens[sorted_indices]
+    does for any token matrix (cuda/triton_token_routed.py:55)."""
+    from complexity_deep.token_routed_mlp import permute_rows, unpermute_rows
+    print(f"permute rows W={W} {dtype} offset={offset}", flush=True)
+    T = 3001
+    g = torch.Generator().manual_seed(W)
+    if dtype.is_floating_point:
+        full = torch.randn(T * W + offset, generator=g).to(dtype)
+    else:
+        full = torch.randint(0, 100, (T * W + offset,), generator=g).to(dtype)
+    x = full[offset:].view(T, W).cuda() if offset == 0 else full.cuda()[offset:].view(T, W)
+    perm = torch.randperm(T, generator=g).to(torch.int32).cuda()
+    out = permute_rows(x, perm)
+    assert torch.equal(out, x[perm.long()])
+    assert torch.equal(unpermute_rows(out, perm), x)
+    eids = torch.randint(0, 5, (T,), generator=g).cuda()
+    sorted_x, idx, _, _ = cdx.sort_tokens_by_expert(x.reshape(T, W), eids, 5)
+    assert torch.equal(sorted_x, x[idx])
