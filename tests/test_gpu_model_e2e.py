@@ -278,6 +278,14 @@ def test_graphed_forward_sees_writes_and_refuses_moved_weights(cdx):
     m.to(torch.bfloat16)
     with pytest.raises(RuntimeError, match="moved since capture"):
         graphed(ids)
+    # a replaced submodule is refused as well (capture again, and it replays)
+    graphed = m.capture_forward(2, 64)
+    with torch.inference_mode():
+        assert torch.equal(graphed(ids), m(ids).logits)
+    m.layers[1].mlp = type(m.layers[1].mlp)(cfg.hidden_size, cfg.intermediate_size, num_experts=cfg.num_experts,
+                                              vocab_size=cfg.vocab_size).to("cuda", torch.bfloat16)
+    with pytest.raises(RuntimeError, match="moved since capture"):
+        graphed(ids)
 
 
 def test_forward_has_no_host_sync(cdx):
