@@ -7,13 +7,18 @@ raises instead of silently returning an output with no gradient path.
 
 from __future__ import annotations
 
+from typing import Optional
+
 import torch
 
 
-def forward_only(what: str, *tensors) -> None:
+def forward_only(what: str, *tensors, module: Optional[torch.nn.Module] = None) -> None:
+    """Raise if autograd would record through a kernel call: grad mode on and any of
+    ``tensors`` (or of ``module``'s parameters, walked only in grad mode) requiring grad."""
     if not torch.is_grad_enabled():
         return
-    for t in tensors:
+    params = module.parameters() if module is not None else ()
+    for t in (*tensors, *params):
         if isinstance(t, torch.Tensor) and t.requires_grad:
             raise NotImplementedError(
                 f"{what}: the MI355X kernels are forward-only (no backward); run the model under "

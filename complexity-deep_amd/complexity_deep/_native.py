@@ -92,16 +92,22 @@ def set_launch_hook(hook: Optional[Callable]) -> None:
     _launch_hook = hook
 
 
-@contextlib.contextmanager
-def launch_region(name: str, device: torch.device, **shape):
-    """Bracket the launches of one C-ABI call with timing events (when hooked).
+class _NoRegion:
+    """The region of an unhooked launch: nothing to record."""
+    __slots__ = ()
 
-    The events go on the device's current torch stream, which is the stream every
-    entry point is given (stream_of)."""
-    hook = _launch_hook
-    if hook is None:
-        yield
-        return
+    def __enter__(self):
+        return None
+
+    def __exit__(self, *exc):
+        return False
+
+
+_NO_REGION = _NoRegion()
+
+
+@contextlib.contextmanager
+def _timed_region(hook, name: str, device: torch.device, shape: dict):
     s = torch.cuda.current_stream(device)
     e0 = torch.cuda.Event(enable_timing=True)
     e1 = torch.cuda.Event(enable_timing=True)
@@ -109,6 +115,18 @@ def launch_region(name: str, device: torch.device, **shape):
     yield
     e1.record(s)
     hook(name, e0, e1, shape)
+
+
+def launch_region(name: str, device: torch.device, **shape):
+    """Bracket the launches of one C-ABI call with timing events (when hooked).
+
+    The events go on the device's current torch stream, which is the stream every
+    entry point is given (stream_of).  Unhooked (the default) it is a shared no-op
+    context, so that a launch pays no generator set-up."""
+    hook = _launch_hook
+    if hook is None:
+        return _NO_REGION
+    return _timed_region(hook, name, device, shape)
 
 
 def exported_symbols():
@@ -122,7 +140,10 @@ def check(rc: int, what: str) -> None:
 
 
 def stream_of(t: torch.Tensor) -> int:
-    return torch.cuda.current_stream(t.device).cuda_stream
+    """The raw hipStream_t of the current torch stream on t's device (what
+    torch.cuda.current_stream(t.device).cuda_stream returns, without building a Stream
+    object on every launch)."""
+    return torch._C._cuda_getCurrentRawStream(t.device.index)
 
 
 def ptr(t: Optional[torch.Tensor]) -> Optional[int]:

@@ -241,7 +241,7 @@ class FusedMuQKVProjection(nn.Module):
         self._qkv_w = QKVWeights()
 
     def forward(self, x: torch.Tensor, mu: Optional[torch.Tensor] = None):
-        forward_only("FusedMuQKVProjection", x, mu, *self.parameters())
+        forward_only("FusedMuQKVProjection", x, mu, module=self)
         w_x, w_mu = self._qkv_w.get(self)
         out = mu_qkv_project(x, mu, w_x, self.hidden_size, w_mu=w_mu)
         return (out[..., : self.q_dim], out[..., self.q_dim: self.q_dim + self.kv_dim],
@@ -362,7 +362,7 @@ class ComplexityAttention(nn.Module):
                 residual: Optional[torch.Tensor] = None):
         """Returns (o_proj(attention), new_kv); with ``residual`` (the block input h,
         contiguous) the output is added to it in place and residual is returned."""
-        forward_only("ComplexityAttention", hidden_states, mu_prev, residual, *self.parameters())
+        forward_only("ComplexityAttention", hidden_states, mu_prev, residual, module=self)
         B, S, _ = hidden_states.shape
         D = self.head_dim
         past_len = past_key_value[0].shape[2] if past_key_value is not None else 0

@@ -63,7 +63,7 @@ class MuGuidance(nn.Module):
         nn.init.zeros_(self.mu_proj.weight)
 
     def fused(self, hidden_states: torch.Tensor, lo: float = -math.inf, hi: float = math.inf) -> torch.Tensor:
-        forward_only("MuGuidance", hidden_states, *self.parameters())
+        forward_only("MuGuidance", hidden_states, module=self)
         return mu_guidance(hidden_states, self.mu_proj.weight, self.mu, self.mu_min, self.mu_max, lo, hi)
 
     def forward(self, hidden_states: torch.Tensor) -> torch.Tensor:

@@ -46,7 +46,7 @@ class SwiGLU(nn.Module):
     def forward(self, x: torch.Tensor, residual: Optional[torch.Tensor] = None) -> torch.Tensor:
         """``residual`` (same shape, contiguous) receives residual + MLP(x) in place and is
         returned (the block's residual add fused into the down pass)."""
-        forward_only("SwiGLU", x, residual, *self.parameters())
+        forward_only("SwiGLU", x, residual, module=self)
         nat.require_device(x, what="SwiGLU")
         w_gu, w_down = self.kernel_weights()
         shape = x.shape

@@ -215,7 +215,7 @@ class ComplexityModel(nn.Module):
                 labels: Optional[torch.Tensor] = None,
                 past_key_values: Optional[List[Tuple[torch.Tensor, torch.Tensor]]] = None,
                 use_cache: bool = False) -> CausalLMOutput:
-        forward_only("ComplexityModel", *self.parameters())
+        forward_only("ComplexityModel", module=self)
         B, S = input_ids.shape
         h = embedding(input_ids, self.embed_tokens.weight)
         mu_prev = self.mu_init.expand(B, S, -1) if self.config.use_mu_guidance else None

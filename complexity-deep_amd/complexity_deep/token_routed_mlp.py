@@ -490,7 +490,7 @@ class TokenRoutedMLP(nn.Module):
         (ComplexityModel computes every layer's in one call).  ``residual`` (same
         shape, contiguous) receives residual + MLP(x) in place and is returned: the
         block's residual add (core/layer.py:183) fused into the down pass."""
-        forward_only("TokenRoutedMLP", hidden_states, residual, *self.parameters())
+        forward_only("TokenRoutedMLP", hidden_states, residual, module=self)
         nat.require_device(hidden_states, what="TokenRoutedMLP")
         shape = hidden_states.shape
         H = shape[-1]
