@@ -2,7 +2,9 @@
 tied LM head (models/modeling.py:74,101-103,177,206).
 
 ``embedding(ids, table)`` is nn.Embedding's lookup through cdx_embedding_fwd (an
-exact row copy; ids outside [0, vocab) give zero rows where nn.Embedding raises).
+exact row copy).  An id outside [0, vocab) gives a row of NaNs where nn.Embedding
+raises: raising would need a host round trip, and the NaNs make every logit that
+depends on the token NaN instead of a plausible number.
 ``linear(x, w)`` is a bias-free nn.Linear (x @ w^T, w stored [out, in]) through the
 MFMA tile engine (cdx_linear_fwd; fp32 accumulation, one bf16 rounding).
 """

@@ -6,8 +6,10 @@
 // Design: one wave64 per token row.  The id is read once per wave (wave-uniform, so
 // the row base is scalar), then every lane copies 16-byte chunks of the row: all
 // loads of a lane first, then all stores, so a wave keeps the whole row in flight.
-// An id outside [0, vocab) yields a zero row (nn.Embedding raises there; a kernel
-// cannot, so the outcome is defined instead of reading out of bounds).
+// An id outside [0, vocab) yields a row of bf16 quiet NaNs.  nn.Embedding raises
+// there, which a kernel cannot do without a host round trip; a NaN row reads nothing
+// out of bounds and cannot pass for a result: every logit that depends on the token
+// (its own row, and through attention every later position of its sequence) is NaN.
 #include "cdx_common.h"
 
 namespace cdx {
@@ -27,11 +29,12 @@ __global__ __launch_bounds__(256) void embedding_kernel(const int64_t* __restric
   const int nvec = H >> 3;
   const uint4* src = reinterpret_cast<const uint4*>(table + (valid ? id : 0) * (int64_t)H);
   uint4* dst = reinterpret_cast<uint4*>(out + row * (int64_t)H);
+  constexpr uint32_t kNaN2 = 0x7FC07FC0u;  // two bf16 quiet NaNs
   uint4 v[VPL];
 #pragma unroll
   for (int i = 0; i < VPL; ++i) {
     const int idx = i * kWave + lane;
-    v[i] = make_uint4(0u, 0u, 0u, 0u);
+    v[i] = make_uint4(kNaN2, kNaN2, kNaN2, kNaN2);
     if (valid && idx < nvec) v[i] = src[idx];
   }
 #pragma unroll

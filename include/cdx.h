@@ -330,7 +330,8 @@ int cdx_binpack_map(const float* freq, int64_t V, int32_t E, int64_t* map);
 /*
  * out[t, :] = table[ids[t], :] for t < T; table [V, H] bf16 (the embedding weight),
  * ids int64 on the device, out [T, H] bf16.  An id outside [0, V) yields a row of
- * zeros (nn.Embedding raises there).  H must be a multiple of 8 and <= 16384.
+ * bf16 quiet NaNs (0x7FC0), so that every output depending on it is NaN: nn.Embedding
+ * raises there, which needs a host round trip.  H must be a multiple of 8 and <= 16384.
  *
  * Replaces: models/modeling.py:74,177 (nn.Embedding and its lookup).
  */

@@ -3,7 +3,7 @@ tied LM head GEMM (cdx_linear_fwd).
 
 References: the embedding is an exact row copy, so it is checked bit for bit against
 torch indexing of the same table (models/modeling.py:177), including ids outside
-[0, vocab), which give zero rows.  The LM head is checked against the fp32 product
+[0, vocab), which give NaN rows (nn.Embedding raises there).  The LM head is checked against the fp32 product
 x.float() @ w.float().T (models/modeling.py:206) at the bf16 tolerance of
 tests/_metrics.py, on configuration 4's shape (16384 tokens, hidden 2048, vocab
 32000: the head of every 1B forward) and on ragged shapes; the model path is covered
@@ -44,7 +44,34 @@ def test_embedding_batched_ids_and_out_of_range(cdx):
     assert out.shape == (2, 4, H)
     ok = (ids >= 0) & (ids < V)
     assert torch.equal(out[ok], table[ids[ok]])
-    assert torch.count_nonzero(out[~ok]) == 0
+    assert bool(torch.isnan(out[~ok]).all())
+
+
+def test_model_out_of_range_id_poisons_only_what_depends_on_it(cdx):
+    """nn.Embedding raises on an id outside [0, vocab); the forward cannot without a host
+    round trip, so the bad token's row is NaN.  Every logit that depends on it (its own
+    position and the later positions of its sequence) must be NaN.  The other sequence and
+    the positions of earlier 128-query attention blocks never read the row and must be
+    bit-identical to the forward with the id clamped (the routing lookup clamps it too).
+    Positions of the bad token's own query block before it are not pinned: their PV
+    product multiplies its NaN V row by a zero probability, as SDPA's would."""
+    torch.manual_seed(0)
+    cfg = cdx.ComplexityConfig(vocab_size=1000, hidden_size=256, intermediate_size=512,
+                               num_hidden_layers=2, num_attention_heads=4, num_key_value_heads=2,
+                               num_experts=4, max_position_embeddings=256)
+    m = cdx.ComplexityModel(cfg).cuda().to(bf16).eval()
+    B, S, p = 2, 256, 200
+    ids = torch.randint(0, cfg.vocab_size, (B, S), device="cuda")
+    bad = ids.clone()
+    bad[1, p] = cfg.vocab_size + 5
+    with torch.no_grad():
+        got = m(bad).logits.float()
+        ref = m(bad.clamp(0, cfg.vocab_size - 1)).logits.float()
+    torch.cuda.synchronize()
+    assert bool(torch.isnan(got[1, p:]).all())
+    assert torch.equal(got[1, :128], ref[1, :128])
+    assert torch.equal(got[0], ref[0])
+    assert not bool(torch.isnan(ref).any())
 
 
 @pytest.mark.parametrize("M,K,N", [(16384, 2048, 32000), (300, 768, 1000), (1, 64, 8), (513, 128, 264)])
