@@ -20,7 +20,17 @@ What it restates (reference file:line it follows):
   ``grouped_gemm``     cuda/triton_token_routed.py:64-86
   ``attention``        core/attention.py:115-181, core/rotary.py:30-86
   ``causal_attention`` core/attention.py:162-181 (the attention core)
+  ``attention_half``   core/layer.py:165-174 (norm, attention, residual add)
+  ``mlp_half``         core/layer.py:176-183 (norm, MLP, residual add)
+  ``mu_out``           core/layer.py:54-61, models/modeling.py:199-200
+  ``layer``            core/layer.py:141-190 (the two halves, then mu)
   ``forward``          models/modeling.py:176-206, core/layer.py:54-61,141-190
+
+``forward`` is nothing but the embedding lookup, ``layer`` per block (itself
+``attention_half``, ``mlp_half`` and ``mu_out``) and the final norm and head, so the
+golden logits that pin ``forward`` pin those four pieces too: a dropped term or a
+wrong index in any of them moves the logits of every configuration the golden test
+holds.
 
 How each function is pinned (independently of its own formula) is listed in the
 tests: tests/test_oracle_routing.py, tests/test_oracle_float.py and
