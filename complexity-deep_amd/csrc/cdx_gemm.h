@@ -139,14 +139,20 @@ constexpr int kNumXcd = 8;
 // DMA_EVERY / DMA_OFF place the refill DMA instructions of a K step behind MFMAs
 // DMA_OFF, DMA_OFF + DMA_EVERY, ... of its last sub-step (1, 0 = a burst behind the
 // first ones); READ_EVERY likewise spaces the fragment reads.
-template <int BN_, int BK_, int STAGES_, int MINB_, int DMA_EVERY_ = 1, int DMA_OFF_ = 0, int READ_EVERY_ = 1>
+// BM rows per tile: 256 (waves of 128 rows), or 128 (waves of 64 rows) for products
+// whose 256-row tiles leave most CUs idle.  The tile shape does not change any output
+// element's accumulation (the same MFMAs over the same K order), so every shape gives
+// the same bits.
+template <int BN_, int BK_, int STAGES_, int MINB_, int DMA_EVERY_ = 1, int DMA_OFF_ = 0, int READ_EVERY_ = 1,
+          int BM_ = kBM>
 struct GemmCfg {
-  static constexpr int BN = BN_, BK = BK_, STAGES = STAGES_, MINB = MINB_;
+  static constexpr int BM = BM_, BN = BN_, BK = BK_, STAGES = STAGES_, MINB = MINB_;
   static constexpr int DMA_EVERY = DMA_EVERY_, DMA_OFF = DMA_OFF_, READ_EVERY = READ_EVERY_;
   static_assert(DMA_OFF < DMA_EVERY, "DMA slot offset must be below its spacing");
+  static_assert(BM == 256 || BM == 128, "BM must be 128 or 256");
   static_assert(BN == 256 || BN == 128 || BN == 64, "BN must be 64, 128 or 256");
   static_assert(BK == 64, "BK must be 64 (two K32 sub-steps per stage)");
-  static constexpr int STAGE_BYTES = (kBM + BN) * BK * 2;
+  static constexpr int STAGE_BYTES = (BM + BN) * BK * 2;
   static_assert(STAGES >= 2 && STAGES * STAGE_BYTES * MINB <= 160 * 1024, "stages must fit 160 KB of LDS");
 };
 #ifndef CDX_GEMM_CFG
@@ -306,15 +312,16 @@ __device__ __forceinline__ uint2 vt_quad_transpose(float x0, float x1, float x2,
 template <class Cfg, ALoad AL, Epi EP, int HD = 0>
 __global__ __launch_bounds__(kGemmThreads, Cfg::MINB) void gemm_nt_kernel(const GemmParams p) {
   constexpr int kBN = Cfg::BN, kBK = Cfg::BK, kStages = Cfg::STAGES;
+  constexpr int kTM = Cfg::BM;                      // rows per tile
   constexpr int ROW_BYTES = kBK * 2;                // bytes per tile row in LDS
   constexpr int CPR = kBK / 8;                      // 16-byte chunks per row
   constexpr int RPL = 256 / ROW_BYTES;              // rows per 256-byte bank line (64 banks)
-  constexpr int A_TILE_BYTES = kBM * ROW_BYTES;     // one stage of A
+  constexpr int A_TILE_BYTES = kTM * ROW_BYTES;     // one stage of A
   constexpr int STAGE_BYTES = Cfg::STAGE_BYTES;     // A then B
-  constexpr int WM = kBM / 2, WN = kBN / 2;
+  constexpr int WM = kTM / 2, WN = kBN / 2;
   constexpr int MI = WM / 16, NI = WN / 16;         // blocks of 16 x 16 per wave
   constexpr int ROWS_PER_DMA = 1024 / ROW_BYTES;    // rows one wave instruction fills
-  constexpr int LD_A = kBM / ROWS_PER_DMA / 4;      // DMA instructions per wave and K step, A
+  constexpr int LD_A = kTM / ROWS_PER_DMA / 4;      // DMA instructions per wave and K step, A
   constexpr int LD_B = kBN / ROWS_PER_DMA / 4;      // and B
   constexpr int LD_PER_STEP = LD_A + LD_B;
   constexpr int NSUB = kBK / 32;                    // K32 sub-steps per K step
@@ -326,9 +333,9 @@ __global__ __launch_bounds__(kGemmThreads, Cfg::MINB) void gemm_nt_kernel(const 
   static_assert(LD_PER_STEP * (kStages - 1) <= 63, "vmcnt range");
 
   // Scatter epilogues: after the stages, the output row (permutation entry) of each of
-  // the tile's kBM rows, loaded in the prologue.
+  // the tile's kTM rows, loaded in the prologue.
   constexpr bool kScatterRows = EP == Epi::kScatter || EP == Epi::kScatterAdd;
-  __shared__ __attribute__((aligned(1024))) uint8_t lds[kStages * STAGE_BYTES + (kScatterRows ? kBM * 4 : 0)];
+  __shared__ __attribute__((aligned(1024))) uint8_t lds[kStages * STAGE_BYTES + (kScatterRows ? kTM * 4 : 0)];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -350,7 +357,7 @@ __global__ __launch_bounds__(kGemmThreads, Cfg::MINB) void gemm_nt_kernel(const 
   int mt_real = p.mt_count;
   if (AL != ALoad::kSegmented && p.offsets != nullptr) {
     mt_real = 0;
-    for (int x = 0; x < p.E; ++x) mt_real += max(0, (seg_off(x + 1) - seg_off(x) + kBM - 1) / kBM);
+    for (int x = 0; x < p.E; ++x) mt_real += max(0, (seg_off(x + 1) - seg_off(x) + kTM - 1) / kTM);
     mt_real = min(mt_real, p.mt_count);
   }
   const int L = xcd_remap(blockIdx.x, mt_real * p.nt_count);
@@ -366,7 +373,7 @@ __global__ __launch_bounds__(kGemmThreads, Cfg::MINB) void gemm_nt_kernel(const 
   const int mt = __builtin_amdgcn_readfirstlane(first_m + in_group % gsz);
   const int nt = __builtin_amdgcn_readfirstlane(in_group / gsz);
 
-  // The tile computes rows [m0, m0 + kBM) and stores rows [m_lo, m_end).
+  // The tile computes rows [m0, m0 + kTM) and stores rows [m_lo, m_end).
   int64_t m0, m_end, m_lo;
   int e = 0;
   int e_lo = 0, n_exp = 1;  // kSegmented: first expert of the tile, experts it touches
@@ -375,10 +382,10 @@ __global__ __launch_bounds__(kGemmThreads, Cfg::MINB) void gemm_nt_kernel(const 
   int seg_lane = 0;
   if constexpr (AL == ALoad::kSegmented) {
     // Rows outside [offsets[0], offsets[E]) belong to no expert and are not stored.
-    m0 = (int64_t)mt * kBM;
+    m0 = (int64_t)mt * kTM;
     seg_lane = lane < p.E ? seg_off(lane) : (int)p.M;
     m_lo = max(m0, (int64_t)__builtin_amdgcn_readfirstlane(seg_lane));
-    m_end = min(min(p.M, m0 + kBM), (int64_t)__builtin_amdgcn_readfirstlane(seg_off(p.E)));
+    m_end = min(min(p.M, m0 + kTM), (int64_t)__builtin_amdgcn_readfirstlane(seg_off(p.E)));
     if (m_lo >= m_end) return;
     // Experts holding rows m_lo and m_end - 1: for consecutive sorted segments, the
     // number of segments after the first that start at or before the row (a segment
@@ -394,10 +401,10 @@ __global__ __launch_bounds__(kGemmThreads, Cfg::MINB) void gemm_nt_kernel(const 
     e = -1;
     for (int x = 0; x < p.E; ++x) {
       const int s0 = seg_off(x), s1 = seg_off(x + 1);
-      const int ntile = max(0, (s1 - s0 + kBM - 1) / kBM);
+      const int ntile = max(0, (s1 - s0 + kTM - 1) / kTM);
       if (mt < before + ntile) {
         e = x;
-        m0 = s0 + (int64_t)(mt - before) * kBM;
+        m0 = s0 + (int64_t)(mt - before) * kTM;
         m_end = s1;
         break;
       }
@@ -406,7 +413,7 @@ __global__ __launch_bounds__(kGemmThreads, Cfg::MINB) void gemm_nt_kernel(const 
     if (e < 0) return;
     m_lo = m0;
   } else {
-    m0 = (int64_t)mt * kBM;
+    m0 = (int64_t)mt * kTM;
     m_end = p.M;
     m_lo = m0;
     if (m0 >= m_end) return;
@@ -459,7 +466,7 @@ __global__ __launch_bounds__(kGemmThreads, Cfg::MINB) void gemm_nt_kernel(const 
   int a_exp[AL == ALoad::kSegmented ? LD_A : 1];
 #pragma unroll
   for (int j = 0; j < LD_A; ++j) {
-    const int r = wave * (kBM / 4) + j * ROWS_PER_DMA + dr;
+    const int r = wave * (kTM / 4) + j * ROWS_PER_DMA + dr;
     const int dchunk = (lane % CPR) ^ ((r / RPL) % CPR);
     int64_t gm = m0 + r;
     if constexpr (AL == ALoad::kSegmented) {
@@ -496,7 +503,7 @@ __global__ __launch_bounds__(kGemmThreads, Cfg::MINB) void gemm_nt_kernel(const 
       b_off[j] = (uint32_t)(((int64_t)(n - n0) * p.ldb + dchunk * 8) * 2);
     }
   }
-  const int a_dma_off = wave * (kBM / 4) * ROW_BYTES;  // this wave's first DMA block in A
+  const int a_dma_off = wave * (kTM / 4) * ROW_BYTES;  // this wave's first DMA block in A
   const int b_dma_off = A_TILE_BYTES + wave * (kBN / 4) * ROW_BYTES;
 
   // Where K step kt reads: k0 = its first K column (the same for A and B), and for
@@ -669,19 +676,19 @@ __global__ __launch_bounds__(kGemmThreads, Cfg::MINB) void gemm_nt_kernel(const 
   };
 
   // Prologue: steps 0 .. kStages-1 in flight, step 0 landed.  Scatter epilogues: thread
-  // r < kBM first loads row r's permutation entry, which lands with step 0 and goes to
+  // r < kTM first loads row r's permutation entry, which lands with step 0 and goes to
   // LDS, so that the epilogue's residual loads need no dependent global load.
   // Entries are clamped into [0, M) (a corrupt permutation scrambles rows but stays in
   // C); rows past the segment repeat its last row's (read, never stored).
   int32_t* perm_lds = reinterpret_cast<int32_t*>(lds + kStages * STAGE_BYTES);
   int32_t perm_pre = 0;
   if constexpr (kScatterRows) {
-    if (tid < kBM) perm_pre = p.perm[m0 + tid < m_end ? m0 + tid : m_end - 1];
+    if (tid < kTM) perm_pre = p.perm[m0 + tid < m_end ? m0 + tid : m_end - 1];
   }
   for (int i = 0; i < kStages; ++i) issue(i, i);
   __builtin_amdgcn_s_waitcnt(waitcnt_imm(LD_PER_STEP * (kStages - 1), 15));
   if constexpr (kScatterRows) {
-    if (tid < kBM) perm_lds[tid] = perm_pre < 0 ? 0 : (perm_pre >= (int32_t)p.M ? (int32_t)p.M - 1 : perm_pre);
+    if (tid < kTM) perm_lds[tid] = perm_pre < 0 ? 0 : (perm_pre >= (int32_t)p.M ? (int32_t)p.M - 1 : perm_pre);
   }
   __syncthreads();
   read_frags(0, 0, 0);
@@ -757,8 +764,11 @@ __global__ __launch_bounds__(kGemmThreads, Cfg::MINB) void gemm_nt_kernel(const 
   }
   // kQKRope, V^T output: a wave whose columns are all V heads and whose WM rows are
   // one run of tokens of one sequence starting at a multiple of 16 stages V^T through
-  // LDS (rows d of 256 bytes = its WM tokens in vt_col order) and stores whole row
+  // LDS (rows d of 2 WM bytes = its WM tokens in vt_col order) and stores whole row
   // segments; other waves store V^T element by element.
+  constexpr int VT_ROWB = WM * 2, VT_CH = VT_ROWB / 16;  // staged V^T row: bytes, 16-byte chunks
+  static_assert(EP != Epi::kQKRope || WN * VT_ROWB <= WM * OUT_ROWB,
+                "staged V^T rows must fit the wave's staging region");
   bool vt_fast = false;
   if constexpr (EP == Epi::kQKRope) {
     vt_fast = p.qk.vt_ld > 0 && n0 + wn * WN >= (p.qk.nq + p.qk.nkv) * HD && (tok_s0 & 15) == 0 &&
@@ -859,12 +869,12 @@ __global__ __launch_bounds__(kGemmThreads, Cfg::MINB) void gemm_nt_kernel(const 
             for (int nb = 0; nb < BPH; ++nb) {
               const uint2 w = vt_quad_transpose(x[nb][0], x[nb][1], x[nb][2], x[nb][3], lane);
               // Tokens r .. r + 3 (r = 16 mi + 4 j) sit at V^T positions
-              // 16 mi + 4 sigma(j) .. + 3; rows are 256 bytes with 16-byte chunk k
-              // at position k ^ (row % 16).
+              // 16 mi + 4 sigma(j) .. + 3; rows are VT_ROWB bytes with 16-byte chunk
+              // k at position k ^ (row % VT_CH).
               const int row = hb * HD + nb * 16 + 4 * q4 + t;
               const int sj = j == 1 ? 2 : (j == 2 ? 1 : j);
               const int chunk = 2 * mi + (sj >> 1);
-              *reinterpret_cast<uint2*>(ep + row * 256 + ((chunk ^ (row & 15)) << 4) + (sj & 1) * 8) = w;
+              *reinterpret_cast<uint2*>(ep + row * VT_ROWB + ((chunk ^ (row & (VT_CH - 1))) << 4) + (sj & 1) * 8) = w;
             }
             continue;
           }
@@ -956,17 +966,17 @@ __global__ __launch_bounds__(kGemmThreads, Cfg::MINB) void gemm_nt_kernel(const 
   __builtin_amdgcn_s_waitcnt(waitcnt_imm(63, 0));
   if constexpr (EP == Epi::kQKRope) {
     if (vt_fast) {
-      // V^T rows: 16 lanes per 256-byte row, four rows per instruction.
-      static_assert(WM * 2 == 256, "a staged V^T row holds the wave's WM tokens in 256 bytes");
+      // V^T rows: VT_CH lanes per row, 64 / VT_CH rows per instruction.
       const QKRopeParams& q = p.qk;
-      const int k = lane & 15;
+      constexpr int VT_RPI = 64 / VT_CH;
+      const int k = lane % VT_CH;
 #pragma unroll 4
-      for (int i = 0; i < WN / 4; ++i) {
-        const int row = i * 4 + (lane >> 4);
+      for (int i = 0; i < WN / VT_RPI; ++i) {
+        const int row = i * VT_RPI + lane / VT_CH;
         const int c0 = n0 + wn * WN + (row / HD) * HD;
         if (c0 >= p.N) continue;
         const int head = (c0 - (q.nq + q.nkv) * HD) / HD, d = row % HD;
-        const uint4 v = *reinterpret_cast<const uint4*>(ep + row * 256 + ((k ^ (row & 15)) << 4));
+        const uint4 v = *reinterpret_cast<const uint4*>(ep + row * VT_ROWB + ((k ^ (row & (VT_CH - 1))) << 4));
         uint16_t* dst = q.v_out + ((tok_b0 * q.nkv + head) * HD + d) * q.vt_ld + tok_s0 + k * 8;
         store_nt16(dst, v);
       }

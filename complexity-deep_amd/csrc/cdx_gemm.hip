@@ -12,6 +12,8 @@
 //                        producer of the next layer's mu operand (the parameter is
 //                        read and clamped in the epilogue)
 //   cdx_linear_fwd       y = x @ W^T (the tied LM head)
+#include <type_traits>
+
 #include "cdx_gemm_persist.h"
 
 namespace cdx {
@@ -26,6 +28,14 @@ using NarrowCfg = GemmCfg<128, 64, 3, 1, 4, 1, 1>;
 // need a wave's 64 or more columns together.  Their ten refills per step ride behind
 // every second MFMA.
 using XNarrowCfg = GemmCfg<64, 64, 3, 1, 2, 1, 1>;
+// Tiles of 128 rows (waves of 64 x 64 or 64 x 32) for products whose 256-row tiles
+// leave many CUs idle (the small model's QKV, mu and MLP products): up to twice the
+// blocks, each with half the MFMA work per K step.  Declared for two blocks per CU:
+// with that register budget the compiler keeps the 64 or 32 accumulators of a lane
+// in place through the K loop (for one block per CU it copied a quarter of them
+// between AGPRs on every K step), and the LDS holds two or three stages.
+using SmallCfg = GemmCfg<128, 64, 2, 2, 2, 1, 1, 128>;
+using XSmallCfg = GemmCfg<64, 64, 3, 2, 1, 0, 1, 128>;
 
 template <ALoad AL, Epi EP, class Cfg = DefaultCfg, int HD = 0>
 int launch(GemmParams p, hipStream_t s, const char* name) {
@@ -38,8 +48,20 @@ int launch(GemmParams p, hipStream_t s, const char* name) {
   if constexpr (Cfg::BN == 256 && (EP != Epi::kQKRope || HD <= 64)) {
     if (2 * nb <= device_cu_count()) return launch<AL, EP, NarrowCfg, HD>(p, s, name);
   }
-  if constexpr (Cfg::BN == 128 && EP != Epi::kQKRope && EP != Epi::kSwiGLU) {
+  if constexpr (Cfg::BN == 128 && Cfg::BM == kBM && EP != Epi::kQKRope && EP != Epi::kSwiGLU) {
     if (2 * nb <= device_cu_count()) return launch<AL, EP, XNarrowCfg, HD>(p, s, name);
+  }
+  // 128-row tiles when they all fit one round of blocks.  The M tile count is recounted
+  // for them (for the grouped passes, again an upper bound with one partial tile per
+  // expert).
+  if constexpr (Cfg::BM == kBM && Cfg::BN <= 128) {
+    using Small = std::conditional_t<Cfg::BN == 128, SmallCfg, XSmallCfg>;
+    const bool grouped = p.offsets != nullptr && AL != ALoad::kSegmented;
+    const int64_t mt_small = (p.M + Small::BM - 1) / Small::BM + (grouped ? p.E : 0);
+    if (mt_small * p.nt_count <= device_cu_count()) {
+      p.mt_count = (int32_t)mt_small;
+      return launch<AL, EP, Small, HD>(p, s, name);
+    }
   }
   if (nb > INT32_MAX) return fail(CDX_EUNSUPPORTED, "%s: problem too large (%lld tiles)", name, (long long)nb);
   // The kernel's K loop runs at least once and whole steps only.

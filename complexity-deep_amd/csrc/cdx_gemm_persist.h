@@ -32,7 +32,8 @@ __global__ __launch_bounds__(kGemmThreads, 1) void gemm_persist_kernel(const Gem
                     (kGathered && EP == Epi::kSwiGLU) || (AL == ALoad::kConcat && EP == Epi::kQKRope && HD == 128),
                 "persistent tiles: dense/concat A with store or bias-clamp, gathered A with SwiGLU, or mu-QKV "
                 "with the QK-norm + RoPE epilogue at head dim 128");
-  static_assert(Cfg::STAGES == 2 && Cfg::MINB == 1 && Cfg::BN == 256, "persistent tiles: 256 x 256, two stages");
+  static_assert(Cfg::STAGES == 2 && Cfg::MINB == 1 && Cfg::BN == 256 && Cfg::BM == kBM,
+                "persistent tiles: 256 x 256, two stages");
   constexpr int kBN = Cfg::BN, kBK = Cfg::BK, kStages = 2;
   constexpr int ROW_BYTES = kBK * 2;
   constexpr int CPR = kBK / 8;

@@ -8,7 +8,8 @@ result; a range check on permutation entries once did exactly that to the MoE
 gate/up pass.  This test compiles cdx_gemm.hip to assembly (hipcc, no GPU needed)
 and checks that the K loop of every engine instantiation is free of both and holds
 the expected MFMA count per iteration (two K32 sub-steps of 8 x 8 blocks per wave for
-256 x 256 tiles, of 8 x 4 blocks for the 256 x 128 tiles of small products).  The
+256 x 256 tiles, of (BM / 32) x (BN / 32) blocks for the narrower tiles of small
+products).  The
 persistent form (gemm_persist_kernel) nests its K loop inside the loop over tiles; its
 K-loop block (the one issuing a whole step's 128 MFMAs and 16 DMAs) gets the same
 checks, and the kernel as a whole must not touch scratch memory.
@@ -53,8 +54,10 @@ def test_gemm_k_loops_have_no_register_shuffles(gemm_asm):
         assert len(loops) == 1, f"{name}: expected one MFMA loop, found {len(loops)}"
         loop = loops[0]
         seen += 1
-        bn = int(re.search(r"GemmCfgILi(\d+)", name).group(1))
-        assert loop.count("v_mfma_f32_16x16x32_bf16") == 128 * bn // 256, name
+        cfg = [int(v) for v in re.search(r"GemmCfgI((?:Li\d+E)+)", name).group(1)[2:-1].split("ELi")]
+        bn, bm = cfg[0], (cfg[7] if len(cfg) > 7 else 256)
+        # two K32 sub-steps of (BM/32) x (BN/32) blocks of 16 x 16 per wave
+        assert loop.count("v_mfma_f32_16x16x32_bf16") == 2 * (bm // 32) * (bn // 32), name
         assert "v_accvgpr_read" not in loop and "v_accvgpr_write" not in loop, \
             f"{name}: VGPR/AGPR shuffles inside the K loop"
         assert "scratch_" not in loop and "buffer_store" not in loop, f"{name}: spills inside the K loop"
