@@ -51,14 +51,14 @@ int launch(GemmParams p, hipStream_t s, const char* name) {
   if constexpr (Cfg::BN == 128 && Cfg::BM == kBM && EP != Epi::kQKRope && EP != Epi::kSwiGLU) {
     if (2 * nb <= device_cu_count()) return launch<AL, EP, XNarrowCfg, HD>(p, s, name);
   }
-  // 128-row tiles when they all fit one round of blocks.  The M tile count is recounted
-  // for them (for the grouped passes, again an upper bound with one partial tile per
-  // expert).
+  // 128-row tiles when they are all resident at once (two blocks per CU).  The M tile
+  // count is recounted for them (for the grouped passes, again an upper bound with one
+  // partial tile per expert).
   if constexpr (Cfg::BM == kBM && Cfg::BN <= 128) {
     using Small = std::conditional_t<Cfg::BN == 128, SmallCfg, XSmallCfg>;
     const bool grouped = p.offsets != nullptr && AL != ALoad::kSegmented;
     const int64_t mt_small = (p.M + Small::BM - 1) / Small::BM + (grouped ? p.E : 0);
-    if (mt_small * p.nt_count <= device_cu_count()) {
+    if (mt_small * p.nt_count <= (int64_t)Small::MINB * device_cu_count()) {
       p.mt_count = (int32_t)mt_small;
       return launch<AL, EP, Small, HD>(p, s, name);
     }
