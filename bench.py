@@ -104,7 +104,7 @@ def work_of(name: str, s: dict):
         # causal: query s sees s + 1 keys; QK^T and PV are 2 * D FLOP per (query, key) each
         S = s["S"]
         return 4.0 * s["B"] * s["nq"] * s["D"] * S * (S + 1) / 2, "flop"
-    if name == "lm_head":
+    if name in ("lm_head", "o_proj"):
         return 2.0 * s["M"] * s["K"] * s["N"], "flop"
     if name == "embedding":
         # ids in; one table row read and one output row written per token

@@ -56,6 +56,7 @@ _SIGNATURES = {
     "cdx_binpack_map": (ctypes.c_int, [_vp, _i64, _i32, _vp]),
     "cdx_embedding_fwd": (ctypes.c_int, [_vp, _i64, _vp, _i64, _i32, _vp, _vp]),
     "cdx_linear_fwd": (ctypes.c_int, [_vp, _i64, _vp, _i64, _i64, _i32, _i32, _vp, _i64, _vp]),
+    "cdx_linear_residual_fwd": (ctypes.c_int, [_vp, _i64, _vp, _i64, _i64, _i32, _i32, _vp, _i64, _vp]),
     "cdx_hbm_probe": (ctypes.c_int, [_i32, _vp, _vp, _i64, _vp]),
 }
 

@@ -7,6 +7,9 @@ raises: raising would need a host round trip, and the NaNs make every logit that
 depends on the token NaN instead of a plausible number.
 ``linear(x, w)`` is a bias-free nn.Linear (x @ w^T, w stored [out, in]) through the
 MFMA tile engine (cdx_linear_fwd; fp32 accumulation, one bf16 rounding).
+``linear_residual_(x, w, residual)`` adds such a product to ``residual`` in place, with
+the rounding of a separate bf16 add (cdx_linear_residual_fwd): the attention block's
+o_proj and residual add (core/attention.py:71,181, core/layer.py:174).
 """
 
 from __future__ import annotations
@@ -57,3 +60,25 @@ def linear(x: torch.Tensor, w: torch.Tensor) -> torch.Tensor:
     if n8 != N:
         out = out[:, :N]
     return out.view(*x.shape[:-1], N)
+
+
+def linear_residual_(x: torch.Tensor, w: torch.Tensor, residual: torch.Tensor) -> torch.Tensor:
+    """residual += x @ w^T in place (the product rounded to bf16, then the add), for
+    x [..., K], w [N, K], residual [..., N] contiguous; K % 64 == 0, N % 8 == 0."""
+    nat.require_device(x, w, residual, what="linear_residual_")
+    N, K = w.shape
+    if x.shape[-1] != K:
+        raise ValueError(f"linear_residual_: x has {x.shape[-1]} features, weight expects {K}")
+    if residual.shape[:-1] != x.shape[:-1] or residual.shape[-1] != N:
+        raise ValueError(f"linear_residual_: residual shape {tuple(residual.shape)} does not match "
+                         f"{tuple(x.shape[:-1]) + (N,)}")
+    if not residual.is_contiguous():
+        raise ValueError("linear_residual_: residual must be contiguous (it is updated in place)")
+    x2 = x.reshape(-1, K)
+    x2 = x2 if x2.is_contiguous() else x2.contiguous()
+    w = w if w.is_contiguous() else w.contiguous()
+    with nat.launch_region("o_proj", x.device, M=x2.shape[0], K=K, N=N):
+        nat.check(nat.lib().cdx_linear_residual_fwd(x2.data_ptr(), K, w.data_ptr(), K, x2.shape[0], K, N,
+                                                    residual.data_ptr(), N, nat.stream_of(x)),
+                  "cdx_linear_residual_fwd")
+    return residual

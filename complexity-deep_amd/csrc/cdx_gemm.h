@@ -683,7 +683,11 @@ __global__ __launch_bounds__(kGemmThreads, Cfg::MINB) void gemm_nt_kernel(const 
   int32_t* perm_lds = reinterpret_cast<int32_t*>(lds + kStages * STAGE_BYTES);
   int32_t perm_pre = 0;
   if constexpr (kScatterRows) {
-    if (tid < kTM) perm_pre = p.perm[m0 + tid < m_end ? m0 + tid : m_end - 1];
+    // (No permutation: identity rows, the residual add of a plain product.)
+    if (tid < kTM) {
+      const int64_t r = m0 + tid < m_end ? m0 + tid : m_end - 1;
+      perm_pre = p.perm != nullptr ? p.perm[r] : (int32_t)r;
+    }
   }
   for (int i = 0; i < kStages; ++i) issue(i, i);
   __builtin_amdgcn_s_waitcnt(waitcnt_imm(LD_PER_STEP * (kStages - 1), 15));

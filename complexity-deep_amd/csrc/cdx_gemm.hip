@@ -75,12 +75,14 @@ int launch(GemmParams p, hipStream_t s, const char* name) {
   // pass nb is the launch bound on the per-expert tiles; the kernel counts the real
   // ones.)
   constexpr bool kDenseTiles =
-      (AL == ALoad::kDense || AL == ALoad::kConcat) && (EP == Epi::kStore || EP == Epi::kBiasClamp);
+      ((AL == ALoad::kDense || AL == ALoad::kConcat) && (EP == Epi::kStore || EP == Epi::kBiasClamp)) ||
+      (AL == ALoad::kDense && EP == Epi::kScatterAdd);
   constexpr bool kGatherTiles = AL == ALoad::kGather && EP == Epi::kSwiGLU;
   constexpr bool kRopeTiles = AL == ALoad::kConcat && EP == Epi::kQKRope && HD == 128;
   if constexpr ((kDenseTiles || kGatherTiles || kRopeTiles) && Cfg::BN == 256) {
     const int64_t grid = (device_cu_count() + kNumXcd - 1) / kNumXcd * kNumXcd;
     bool whole = kGatherTiles ? p.offsets != nullptr : (p.offsets == nullptr && p.M % kBM == 0);
+    if (EP == Epi::kScatterAdd) whole = whole && p.perm == nullptr;  // identity rows only
     if (kRopeTiles) whole = whole && p.qk.vt_ld > 0 && p.qk.S % (kBM / 2) == 0;
     if (whole && p.N % Cfg::BN == 0 && p.K >= 2 * Cfg::BK && nb > grid) {
       gemm_persist_kernel<Cfg, AL, EP, HD><<<dim3((unsigned)grid), dim3(kGemmThreads), 0, s>>>(p);
@@ -437,4 +439,38 @@ extern "C" int cdx_linear_fwd(const uint16_t* x, int64_t ldx, const uint16_t* w,
   if (cdiv(M, kBM) > INT32_MAX) return fail(CDX_EUNSUPPORTED, "%s: M too large", name);
   p.mt_count = (int32_t)cdiv(M, kBM);
   return launch<ALoad::kDense, Epi::kStore>(p, reinterpret_cast<hipStream_t>(stream), name);
+}
+
+extern "C" int cdx_linear_residual_fwd(const uint16_t* x, int64_t ldx, const uint16_t* w, int64_t ldw, int64_t M,
+                                       int32_t K, int32_t N, uint16_t* residual, int64_t ldr, void* stream) {
+  using namespace cdx;
+  clear_error();
+  const char* name = "cdx_linear_residual_fwd";
+  if (M < 0 || K <= 0 || N <= 0) return fail(CDX_EINVAL, "%s: bad shape M=%lld K=%d N=%d", name, (long long)M, K, N);
+  if (K % 64 != 0) return fail(CDX_EUNSUPPORTED, "%s: K=%d must be a multiple of 64", name, K);
+  // The residual is read and written in whole 16-byte pieces.
+  if (N % 8 != 0) return fail(CDX_EUNSUPPORTED, "%s: N=%d must be a multiple of 8", name, N);
+  if (M > INT32_MAX) return fail(CDX_EUNSUPPORTED, "%s: M=%lld too large", name, (long long)M);
+  if (ldx < K || ldw < K || ldr < N) return fail(CDX_EINVAL, "%s: leading dimension too small", name);
+  if (ldx % 8 || ldw % 8 || ldr % 8)
+    return fail(CDX_EUNSUPPORTED, "%s: leading dimensions must be multiples of 8", name);
+  if (M == 0) return CDX_OK;
+  if (!x || !w || !residual) return fail(CDX_EINVAL, "%s: null pointer", name);
+  if (!aligned16(x) || !aligned16(w) || !aligned16(residual))
+    return fail(CDX_EUNSUPPORTED, "%s: pointers must be 16-byte aligned", name);
+  GemmParams p{};
+  p.a = x;
+  p.lda = ldx;
+  p.k_split = 0;     // every K column from b (the residual-add kernels' B has no shared block)
+  p.perm = nullptr;  // identity rows
+  p.E = 1;
+  p.M = M;
+  p.b = w;
+  p.ldb = ldw;
+  p.N = N;
+  p.K = K;
+  p.c = residual;
+  p.ldc = ldr;
+  p.mt_count = (int32_t)cdiv(M, kBM);
+  return launch<ALoad::kDense, Epi::kScatterAdd>(p, reinterpret_cast<hipStream_t>(stream), name);
 }

@@ -28,10 +28,13 @@ namespace cdx {
 template <class Cfg, ALoad AL, Epi EP, int HD = 0>
 __global__ __launch_bounds__(kGemmThreads, 1) void gemm_persist_kernel(const GemmParams p) {
   constexpr bool kGathered = AL == ALoad::kGather;
+  // kScatterAdd here has identity rows (no permutation): c += the tile, the residual
+  // add fused into a plain product.
   static_assert(((AL == ALoad::kDense || AL == ALoad::kConcat) && (EP == Epi::kStore || EP == Epi::kBiasClamp)) ||
-                    (kGathered && EP == Epi::kSwiGLU) || (AL == ALoad::kConcat && EP == Epi::kQKRope && HD == 128),
-                "persistent tiles: dense/concat A with store or bias-clamp, gathered A with SwiGLU, or mu-QKV "
-                "with the QK-norm + RoPE epilogue at head dim 128");
+                    (AL == ALoad::kDense && EP == Epi::kScatterAdd) || (kGathered && EP == Epi::kSwiGLU) ||
+                    (AL == ALoad::kConcat && EP == Epi::kQKRope && HD == 128),
+                "persistent tiles: dense/concat A with store or bias-clamp, dense A with the residual add, "
+                "gathered A with SwiGLU, or mu-QKV with the QK-norm + RoPE epilogue at head dim 128");
   static_assert(Cfg::STAGES == 2 && Cfg::MINB == 1 && Cfg::BN == 256 && Cfg::BM == kBM,
                 "persistent tiles: 256 x 256, two stages");
   constexpr int kBN = Cfg::BN, kBK = Cfg::BK, kStages = 2;
@@ -504,6 +507,15 @@ __global__ __launch_bounds__(kGemmThreads, 1) void gemm_persist_kernel(const Gem
     uint8_t* ep = lds + stage * STAGE_BYTES + wave * (HALF_ROWS * OUT_ROWB);
 #pragma unroll
     for (int h = 0; h < 2; ++h) {
+      uint16_t* crow = p.c + (m0 + wm * WM + h * HALF_ROWS + lane / OUT_CH) * p.ldc + n0 + wn * WN + jc * 8;
+      // Residual add: the half's pieces of c are loaded before the staging, so that
+      // their latency runs under it; each piece belongs to this lane alone.
+      uint4 resid[EP == Epi::kScatterAdd ? HALF_ROWS / RPI : 1];
+      if constexpr (EP == Epi::kScatterAdd) {
+#pragma unroll
+        for (int i = 0; i < HALF_ROWS / RPI; ++i)
+          resid[i] = *reinterpret_cast<const uint4*>(crow + (int64_t)i * RPI * p.ldc);
+      }
 #pragma unroll
       for (int mh = 0; mh < MI / 2; ++mh) {
         const int mi = h * (MI / 2) + mh;
@@ -527,12 +539,20 @@ __global__ __launch_bounds__(kGemmThreads, 1) void gemm_persist_kernel(const Gem
       __builtin_amdgcn_s_waitcnt(waitcnt_imm(63, 0));
       // Each store takes its data from a read of the region, so the region is read
       // in full before the next half overwrites it.
-      uint16_t* crow = p.c + (m0 + wm * WM + h * HALF_ROWS + lane / OUT_CH) * p.ldc + n0 + wn * WN + jc * 8;
+      if constexpr (EP == Epi::kScatterAdd) {
+#pragma unroll
+        for (int i = 0; i < HALF_ROWS / RPI; ++i) {  // resid[] is indexed by constants only
+          const int r = i * RPI + lane / OUT_CH;
+          const uint4 v = *reinterpret_cast<const uint4*>(ep + r * OUT_ROWB + ((jc ^ (r % OUT_CH)) << 4));
+          store_nt16(crow + (int64_t)i * RPI * p.ldc, add_bf16x8(v, resid[i]));
+        }
+      } else {
 #pragma unroll 4
-      for (int i = 0; i < HALF_ROWS / RPI; ++i) {
-        const int r = i * RPI + lane / OUT_CH;
-        const uint4 v = *reinterpret_cast<const uint4*>(ep + r * OUT_ROWB + ((jc ^ (r % OUT_CH)) << 4));
-        store_nt16(crow + (int64_t)i * RPI * p.ldc, v);
+        for (int i = 0; i < HALF_ROWS / RPI; ++i) {
+          const int r = i * RPI + lane / OUT_CH;
+          const uint4 v = *reinterpret_cast<const uint4*>(ep + r * OUT_ROWB + ((jc ^ (r % OUT_CH)) << 4));
+          store_nt16(crow + (int64_t)i * RPI * p.ldc, v);
+        }
       }
     }
   };

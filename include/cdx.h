@@ -351,6 +351,19 @@ int cdx_embedding_fwd(const int64_t* ids_dev, int64_t T, const uint16_t* table_d
 int cdx_linear_fwd(const uint16_t* x_dev, int64_t ldx, const uint16_t* w_dev, int64_t ldw, int64_t M, int32_t K,
                    int32_t N, uint16_t* out_dev, int64_t ldo, void* stream);
 
+/*
+ * residual[M, N] = bf16(residual + bf16(x[M, K] @ w[N, K]^T)), in place: a bias-free
+ * nn.Linear whose bf16 output is added to the residual stream with the rounding of a
+ * separate bf16 add.  The model calls it for o_proj and the block's first residual
+ * add.  K % 64 == 0, N % 8 == 0, M <= INT32_MAX, leading dimensions multiples of 8,
+ * pointers 16-byte aligned.
+ *
+ * Replaces: core/attention.py:71,181 (o_proj) with core/layer.py:174
+ * (hidden_states = residual + hidden_states).
+ */
+int cdx_linear_residual_fwd(const uint16_t* x_dev, int64_t ldx, const uint16_t* w_dev, int64_t ldw, int64_t M,
+                            int32_t K, int32_t N, uint16_t* residual_dev, int64_t ldr, void* stream);
+
 /* ---- measurement ---------------------------------------------------------- */
 
 /*

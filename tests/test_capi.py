@@ -126,6 +126,11 @@ def test_gemm_validation(lib):
     assert lib.cdx_mu_guidance_fwd(16, 8, 64, 16, 16, 2.0, 0.0, -2.0, 2.0, 16, None) == CDX_EINVAL  # mu_lo > mu_hi
     assert lib.cdx_mu_guidance_fwd(16, 8, 64, 16, None, 0.0, 2.0, -2.0, 2.0, 16, None) == CDX_EINVAL  # no mu
     assert lib.cdx_linear_fwd(16, 64, 16, 64, 8, 64, 30, 16, 30, None) == CDX_EINVAL  # ldo < round_up(N, 8)
+    assert lib.cdx_linear_residual_fwd(16, 64, 16, 64, 8, 64, 30, 16, 32, None) == CDX_EUNSUPPORTED  # N % 8
+    assert lib.cdx_linear_residual_fwd(16, 96, 16, 96, 8, 96, 32, 16, 32, None) == CDX_EUNSUPPORTED  # K % 64
+    assert lib.cdx_linear_residual_fwd(16, 64, 16, 64, 8, 64, 32, 16, 16, None) == CDX_EINVAL  # ldr < N
+    assert lib.cdx_linear_residual_fwd(16, 64, 16, 64, 1 << 31, 64, 32, 16, 32, None) == CDX_EUNSUPPORTED  # M
+    assert lib.cdx_linear_residual_fwd(None, 64, None, 64, 0, 64, 32, None, 32, None) == 0  # M = 0
 
 
 def test_cpu_tensors_raise():

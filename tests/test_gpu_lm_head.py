@@ -134,3 +134,27 @@ def test_model_head_odd_vocab_runs_the_kernel(cdx, monkeypatch):
     assert calls == [(1001, 128)]
     assert logits.shape == (2, 24, 1001)
     assert torch.isfinite(logits.float()).all()
+
+
+@pytest.mark.parametrize("M,K,N", [(16384, 2048, 2048), (2048, 768, 768), (300, 128, 264), (513, 64, 8),
+                                   (4096, 1024, 3072)])
+def test_linear_residual_is_the_product_then_a_bf16_add(cdx, M, K, N):
+    """o_proj + the block's residual add (core/attention.py:181, core/layer.py:174): the
+    product rounded to bf16, then added to the residual with a bf16 add.  The product
+    is the tile engine's (the same accumulation as cdx_linear_fwd, whatever the tile
+    shape), so the result is checked bit for bit against linear() plus torch's bf16 add,
+    and the product against the fp32 one at the bf16 tolerance."""
+    from complexity_deep.linear import linear, linear_residual_
+    print(f"linear_residual M={M} K={K} N={N}", flush=True)
+    g = torch.Generator().manual_seed(M + K + N)
+    x = torch.randn(M, K, generator=g).to(bf16).cuda()
+    w = (torch.randn(N, K, generator=g) * 0.02).to(bf16).cuda()
+    r0 = torch.randn(M, N, generator=g).to(bf16).cuda()
+    res = r0.clone()
+    out = linear_residual_(x, w, res)
+    prod = linear(x, w)
+    torch.cuda.synchronize()
+    assert out.data_ptr() == res.data_ptr()
+    assert torch.equal(res, r0 + prod)
+    ref = x.float() @ w.float().t()
+    assert_close_bf16(prod.float(), ref, f"linear_residual product {M}x{K}x{N}")
