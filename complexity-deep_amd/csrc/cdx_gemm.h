@@ -133,7 +133,8 @@ constexpr int kGroupM = CDX_GROUP_M;  // M tiles per group in the tile order
 constexpr int kNumXcd = 8;
 
 // Tile configuration: BN output columns per block, BK-deep LDS stages, STAGES of
-// them in flight, MINB blocks resident per CU.  Stage s holds the A (256 x BK) and B
+// them in flight, compiled for MINB blocks per CU (the launch bound, which sets the
+// register budget; RESIDENT blocks fit the LDS at once).  Stage s holds the A (256 x BK) and B
 // (BN x BK) tiles of one K step; the DMA of step k + STAGES is issued as soon as
 // stage k is consumed, so a load has STAGES - 1 K steps to land.
 // DMA_EVERY / DMA_OFF place the refill DMA instructions of a K step behind MFMAs
@@ -153,7 +154,9 @@ struct GemmCfg {
   static_assert(BN == 256 || BN == 128 || BN == 64, "BN must be 64, 128 or 256");
   static_assert(BK == 64, "BK must be 64 (two K32 sub-steps per stage)");
   static constexpr int STAGE_BYTES = (BM + BN) * BK * 2;
-  static_assert(STAGES >= 2 && STAGES * STAGE_BYTES * MINB <= 160 * 1024, "stages must fit 160 KB of LDS");
+  static_assert(STAGES >= 2 && STAGES * STAGE_BYTES <= 160 * 1024, "stages must fit 160 KB of LDS");
+  static constexpr int RESIDENT = (160 * 1024) / (STAGES * STAGE_BYTES) < MINB ? (160 * 1024) / (STAGES * STAGE_BYTES)
+                                                                                : MINB;
 };
 #ifndef CDX_GEMM_CFG
 #define CDX_GEMM_CFG 256, 64, 2, 1, 4, 1, 1

@@ -30,11 +30,14 @@ using NarrowCfg = GemmCfg<128, 64, 3, 1, 4, 1, 1>;
 using XNarrowCfg = GemmCfg<64, 64, 3, 1, 2, 1, 1>;
 // Tiles of 128 rows (waves of 64 x 64 or 64 x 32) for products whose 256-row tiles
 // leave many CUs idle (the small model's QKV, mu and MLP products): up to twice the
-// blocks, each with half the MFMA work per K step.  Declared for two blocks per CU:
-// with that register budget the compiler keeps the 64 or 32 accumulators of a lane
-// in place through the K loop (for one block per CU it copied a quarter of them
-// between AGPRs on every K step), and the LDS holds two or three stages.
-using SmallCfg = GemmCfg<128, 64, 2, 2, 2, 1, 1, 128>;
+// blocks, each with half the MFMA work per K step.  128 x 128: three stages (96 KB,
+// one block per CU), so that a load has two short K steps to land; in a forward,
+// where each layer's weights come from HBM, that beat two stages by 4% although the
+// register allocator then copies some accumulators between AGPRs on every K step
+// (store, SwiGLU and QK-norm epilogues).  128 x 64: three stages of 24 KB, compiled
+// for two blocks per CU (with that register budget its K loops keep the
+// accumulators in place).
+using SmallCfg = GemmCfg<128, 64, 3, 1, 2, 1, 1, 128>;
 using XSmallCfg = GemmCfg<64, 64, 3, 2, 1, 0, 1, 128>;
 
 template <ALoad AL, Epi EP, class Cfg = DefaultCfg, int HD = 0>
@@ -51,14 +54,14 @@ int launch(GemmParams p, hipStream_t s, const char* name) {
   if constexpr (Cfg::BN == 128 && Cfg::BM == kBM && EP != Epi::kQKRope && EP != Epi::kSwiGLU) {
     if (2 * nb <= device_cu_count()) return launch<AL, EP, XNarrowCfg, HD>(p, s, name);
   }
-  // 128-row tiles when they are all resident at once (two blocks per CU).  The M tile
-  // count is recounted for them (for the grouped passes, again an upper bound with one
-  // partial tile per expert).
+  // 128-row tiles when they are all resident at once (RESIDENT blocks per CU).  The M
+  // tile count is recounted for them (for the grouped passes, again an upper bound
+  // with one partial tile per expert).
   if constexpr (Cfg::BM == kBM && Cfg::BN <= 128) {
     using Small = std::conditional_t<Cfg::BN == 128, SmallCfg, XSmallCfg>;
     const bool grouped = p.offsets != nullptr && AL != ALoad::kSegmented;
     const int64_t mt_small = (p.M + Small::BM - 1) / Small::BM + (grouped ? p.E : 0);
-    if (mt_small * p.nt_count <= (int64_t)Small::MINB * device_cu_count()) {
+    if (mt_small * p.nt_count <= (int64_t)Small::RESIDENT * device_cu_count()) {
       p.mt_count = (int32_t)mt_small;
       return launch<AL, EP, Small, HD>(p, s, name);
     }

