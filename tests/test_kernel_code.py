@@ -86,8 +86,11 @@ def test_persistent_gemm_k_loops_have_no_register_shuffles(gemm_asm):
         start = gemm_asm.index(name + ":")
         body = gemm_asm[start:gemm_asm.index(".Lfunc_end", start)]
         assert "scratch_" not in body, f"{name}: scratch memory in use"
-        k_loops = [txt for _, txt in _blocks(body)
-                   if txt.count("v_mfma_f32_16x16x32_bf16") == 128 and txt.count(" lds") == 16]
+        # The K-loop block branches back to itself (a tile's last step, which can also
+        # carry 16 DMAs, falls through into the epilogue instead).
+        k_loops = [txt for label, txt in _blocks(body)
+                   if txt.count("v_mfma_f32_16x16x32_bf16") == 128 and txt.count(" lds") == 16
+                   and re.search(r"s_cbranch_\w+ " + re.escape(label) + r"\b", txt)]
         assert k_loops, f"{name}: no K-loop block with 128 MFMAs and 16 DMAs"
         for loop in k_loops:
             assert "v_accvgpr_read" not in loop and "v_accvgpr_write" not in loop, \
