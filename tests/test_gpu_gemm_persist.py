@@ -73,15 +73,17 @@ def test_persistent_mu_guidance_many_tiles(cdx):
 
 @pytest.mark.parametrize("K,N", [(768, 768), (2048, 2048), (1536, 1280)])
 def test_tile_forms_agree_bit_for_bit(cdx, K, N):
-    """The engine picks its tile form from the tile count: 256 x 64 tiles (plain
-    epilogues) when even 256 x 128 tiles number at most half the CUs, 256 x 128 tiles
-    when at most half as many 256 x 256 tiles as CUs, one 256 x 256 tile per block up to
-    one per CU, the persistent form beyond.  Every form accumulates an output element
-    over K in the same order, so rows are independent of the form: the first rows of a
-    large product (persistent) equal the product of those rows alone (256 x 64 tiles),
-    of about 96 tiles' worth (256 x 128) and of a middling batch (one tile per block),
-    bit for bit.  Checked for the plain product, the mu-QKV contraction (two K sources)
-    and mu guidance (bias + clamp)."""
+    """The engine picks its tile form from the tile count: 128-row tiles (128 x 128, or
+    128 x 64 for plain epilogues) when all of them are resident at once, else 256 x 64
+    tiles (plain epilogues) when even 256 x 128 tiles number at most half the CUs,
+    256 x 128 tiles when at most half as many 256 x 256 tiles as CUs, one 256 x 256 tile
+    per block up to one per CU, the persistent form beyond.  Every form accumulates an
+    output element over K in the same order, so rows are independent of the form: the
+    first rows of a large product (persistent) equal the product of those rows alone
+    (128-row tiles), of about 96 tiles' worth and of a middling batch (one tile per
+    block), bit for bit.  Checked for the plain product, the product added to a
+    residual (o_proj), the mu-QKV contraction (two K sources) and mu guidance (bias +
+    clamp)."""
     from complexity_deep.attention import mu_qkv_project
     from complexity_deep.layer import mu_guidance
     from complexity_deep.linear import linear
@@ -96,6 +98,13 @@ def test_tile_forms_agree_bit_for_bit(cdx, K, N):
     full = linear(x, w)
     for rows in (256, nar, mid):
         assert torch.equal(linear(x[:rows].contiguous(), w), full[:rows]), f"linear rows={rows}"
+    if K % 64 == 0 and N % 8 == 0:
+        from complexity_deep.linear import linear_residual_
+        r0 = torch.randn(big, N, generator=g).to(bf16).cuda()
+        fr = linear_residual_(x, w, r0.clone())
+        for rows in (256, nar, mid):
+            part = linear_residual_(x[:rows].contiguous(), w, r0[:rows].clone())
+            assert torch.equal(part, fr[:rows]), f"linear_residual rows={rows}"
     H = K // 2
     mu = torch.randn(big, H, generator=g).clamp(-2, 2).to(bf16).cuda()
     wq = (torch.randn(N, 2 * H, generator=g) * 0.05).to(bf16).cuda()
