@@ -207,3 +207,31 @@ def test_qkv_rope_many_tiles(cdx, oracle, B, S, H, nq, nkv, mu_mode, pos0, qk_no
         assert_close_bf16(q[b:b + 1], rq, f"q[{b}]")
         assert_close_bf16(k[b:b + 1], rk, f"k[{b}]")
         assert_close_bf16(v[b:b + 1], rv, f"v[{b}]")
+
+
+@pytest.mark.parametrize("B,S,H,nq,nkv", [(32, 512, 768, 12, 4),    # D = 64: 128 x 128 tiles vs 256 x 256
+                                          (16, 1024, 2048, 16, 8)])  # D = 128: 256 x 256 vs persistent
+def test_qkv_rope_sequences_independent_of_batch(cdx, B, S, H, nq, nkv):
+    """A sequence's q, k and V^T do not depend on the rest of the batch: the first two
+    sequences alone (few tiles: the 128-row tiles at head dim 64, one 256 x 256 tile per
+    block at 128) and inside a batch of B (256-row tiles, the persistent form at head dim
+    128) give the same bits.  Every tile form accumulates an element over K in the same
+    order and runs the same QK-norm + RoPE arithmetic."""
+    from complexity_deep.attention import mu_qkv_rope
+    from complexity_deep.rotary import RotaryEmbedding
+    D = H // nq
+    print(f"qkv_rope sequences independent of batch B={B} S={S} H={H} D={D}", flush=True)
+    g = torch.Generator().manual_seed(B + S + H)
+    x = torch.randn(B, S, H, generator=g).to(bf16).cuda()
+    mu = torch.randn(B, S, H, generator=g).clamp(-2, 2).to(bf16).cuda()
+    N = (nq + 2 * nkv) * D
+    w_pack = (torch.randn(N, 2 * H, generator=g) * 0.02).to(bf16).cuda()
+    qn = (1 + 0.1 * torch.randn(D, generator=g)).to(bf16).cuda()
+    kn = (1 + 0.1 * torch.randn(D, generator=g)).to(bf16).cuda()
+    table = RotaryEmbedding(D).cuda().cos_sin_table(S, torch.device("cuda"))
+    q, k, vt = mu_qkv_rope(x, mu, w_pack, H, nq, nkv, D, qn, kn, 1e-6, table, 0, v_transposed=True)
+    q2, k2, vt2 = mu_qkv_rope(x[:2].contiguous(), mu[:2].contiguous(), w_pack, H, nq, nkv, D, qn, kn, 1e-6, table,
+                              0, v_transposed=True)
+    torch.cuda.synchronize()
+    assert torch.equal(q2, q[:2]) and torch.equal(k2, k[:2])
+    assert torch.equal(vt2[..., :S], vt[:2, ..., :S])
