@@ -36,7 +36,10 @@ from .rotary import RotaryEmbedding, apply_rotary_pos_emb
 
 
 def _rows_view(t: torch.Tensor, H: int) -> Tuple[torch.Tensor, int]:
-    """Express a [..., H] tensor as rows base + r * ld; ld = 0 for one broadcast row."""
+    """Express a [..., H] tensor as rows base + r * ld; ld = 0 for one broadcast row.
+    (Only the base pointer and ld are used: a contiguous tensor is returned as is.)"""
+    if t.shape[-1] == H and t.is_contiguous():
+        return t, H
     if t.stride(-1) != 1:
         t = t.contiguous()
     if t.dim() > 1 and all(s == 0 for s in t.stride()[:-1]):

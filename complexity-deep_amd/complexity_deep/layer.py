@@ -32,15 +32,15 @@ def mu_guidance(h: torch.Tensor, w: torch.Tensor, mu: torch.Tensor, mu_lo: float
     accumulate, one rounding).  h [..., H], w [H, H] and mu [H], all bf16."""
     nat.require_device(h, w, mu, what="mu_guidance")
     H = h.shape[-1]
-    h2 = h.reshape(-1, H)
-    h2 = h2 if h2.is_contiguous() else h2.contiguous()
+    h2 = h if h.is_contiguous() else h.contiguous()  # rows base + r * H
+    T = h2.numel() // H if H else 0
     w = w if w.is_contiguous() else w.contiguous()
     mu = mu if mu.is_contiguous() else mu.contiguous()
     if mu.shape != (H,):
         raise ValueError(f"mu_guidance: mu must be [{H}], got {tuple(mu.shape)}")
     out = torch.empty(h.shape, dtype=h.dtype, device=h.device)
-    with nat.launch_region("mu_guidance", h.device, T=h2.shape[0], H=H):
-        nat.check(nat.lib().cdx_mu_guidance_fwd(h2.data_ptr(), h2.shape[0], H, w.data_ptr(), mu.data_ptr(),
+    with nat.launch_region("mu_guidance", h.device, T=T, H=H):
+        nat.check(nat.lib().cdx_mu_guidance_fwd(h2.data_ptr(), T, H, w.data_ptr(), mu.data_ptr(),
                                                 float(mu_lo), float(mu_hi), float(lo), float(hi), out.data_ptr(),
                                                 nat.stream_of(h)), "cdx_mu_guidance_fwd")
     return out

@@ -74,11 +74,11 @@ def linear_residual_(x: torch.Tensor, w: torch.Tensor, residual: torch.Tensor) -
                          f"{tuple(x.shape[:-1]) + (N,)}")
     if not residual.is_contiguous():
         raise ValueError("linear_residual_: residual must be contiguous (it is updated in place)")
-    x2 = x.reshape(-1, K)
-    x2 = x2 if x2.is_contiguous() else x2.contiguous()
+    x2 = x if x.is_contiguous() else x.contiguous()  # rows base + r * K
+    M = x2.numel() // K if K else 0
     w = w if w.is_contiguous() else w.contiguous()
-    with nat.launch_region("o_proj", x.device, M=x2.shape[0], K=K, N=N):
-        nat.check(nat.lib().cdx_linear_residual_fwd(x2.data_ptr(), K, w.data_ptr(), K, x2.shape[0], K, N,
+    with nat.launch_region("o_proj", x.device, M=M, K=K, N=N):
+        nat.check(nat.lib().cdx_linear_residual_fwd(x2.data_ptr(), K, w.data_ptr(), K, M, K, N,
                                                     residual.data_ptr(), N, nat.stream_of(x)),
                   "cdx_linear_residual_fwd")
     return residual

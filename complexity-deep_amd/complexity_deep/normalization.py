@@ -24,11 +24,6 @@ from . import _native as nat
 from ._grad import forward_only
 
 
-def _as_rows(t: torch.Tensor) -> torch.Tensor:
-    t = t if t.is_contiguous() else t.contiguous()
-    return t.view(-1, t.shape[-1])
-
-
 def _weight(weight: torch.Tensor, like: torch.Tensor) -> torch.Tensor:
     if weight.dtype != like.dtype or weight.device != like.device:
         weight = weight.to(device=like.device, dtype=like.dtype)
@@ -58,25 +53,29 @@ def add_rms_norm(x: torch.Tensor, residual: Optional[torch.Tensor], weight: torc
     nat.require_device(x, residual, what="add_rms_norm")
     shape = x.shape
     H = shape[-1]
-    x2 = _as_rows(x)
+    # The kernel reads rows base + r * H: contiguous operands need no row view.
+    x2 = x if x.is_contiguous() else x.contiguous()
+    T = x2.numel() // H if H else 0
     r2 = None
     if residual is not None:
         if residual.shape != shape:
             raise ValueError(f"add_rms_norm: residual shape {tuple(residual.shape)} != {tuple(shape)}")
-        r2 = _as_rows(residual)
+        r2 = residual if residual.is_contiguous() else residual.contiguous()
     w = _weight(weight, x2)
     if w.numel() != H:
         raise ValueError(f"add_rms_norm: weight has {w.numel()} elements, hidden size is {H}")
-    _check_out(out, x, "out")
-    _check_out(residual_out, x, "residual_out")
+    if out is not None:
+        _check_out(out, x, "out")
+    if residual_out is not None:
+        _check_out(residual_out, x, "residual_out")
     y = out if out is not None else torch.empty(shape, dtype=x.dtype, device=x.device)
     h = None
     if residual is not None and store_residual:
         h = residual_out if residual_out is not None else torch.empty(shape, dtype=x.dtype, device=x.device)
-    with nat.launch_region("add_rmsnorm" if r2 is not None else "rmsnorm", x.device, T=x2.shape[0], H=H,
+    with nat.launch_region("add_rmsnorm" if r2 is not None else "rmsnorm", x.device, T=T, H=H,
                            residual=r2 is not None, store_residual=h is not None):
         nat.check(nat.lib().cdx_add_rmsnorm_fwd(
-            x2.data_ptr(), nat.ptr(r2), w.data_ptr(), float(eps), x2.shape[0], H,
+            x2.data_ptr(), nat.ptr(r2), w.data_ptr(), float(eps), T, H,
             y.data_ptr(), nat.ptr(h), nat.stream_of(x)), "cdx_add_rmsnorm_fwd")
     return y, h
 
