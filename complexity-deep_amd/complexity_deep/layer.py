@@ -4,8 +4,8 @@
 (hidden_states, new_kv, mu) with mu unclamped, as the reference does.  Inside, the
 residual add before the MLP's norm is the fused add+RMSNorm kernel.
 ``ComplexityModel`` drives the blocks through ``forward_fused``, where both residual
-adds run inside the kernels that produce the branch outputs (o_proj's epilogue, the
-MoE down pass's scatter epilogue) and the norms after them are
+adds run inside the kernels that produce the branch outputs (o_proj as hipBLASLt's
+GEMM with beta = 1, the MoE down pass's scatter epilogue) and the norms after them are
 plain RMSNorms of h; the layer's routing plan comes from the model.
 """
 
@@ -127,8 +127,8 @@ class TransformerBlock(nn.Module):
         Returns (h, next_norm(h_out), new_kv, mu) where mu is already clamped to [-2, 2],
         the model's clamp between layers (modeling.py:199-200).  Both residual adds
         (core/layer.py:174, 183) happen inside the kernels that produce the branch
-        outputs: o_proj's epilogue (cdx_linear_residual_fwd) and the MoE down pass's
-        scatter epilogue; the norms that follow read h alone.  ``want_mu=False`` skips mu for
+        outputs: o_proj as a GEMM with beta = 1 and the MoE down pass's scatter
+        epilogue; the norms that follow read h alone.  ``want_mu=False`` skips mu for
         the last layer, whose mu the reference computes and then discards."""
         if not h.is_contiguous():
             raise ValueError("forward_fused: h must be contiguous (it is updated in place)")

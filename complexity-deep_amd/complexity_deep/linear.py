@@ -9,7 +9,9 @@ depends on the token NaN instead of a plausible number.
 MFMA tile engine (cdx_linear_fwd; fp32 accumulation, one bf16 rounding).
 ``linear_residual_(x, w, residual)`` adds such a product to ``residual`` in place, with
 the rounding of a separate bf16 add (cdx_linear_residual_fwd): the attention block's
-o_proj and residual add (core/attention.py:71,181, core/layer.py:174).
+o_proj and residual add (core/attention.py:71,181, core/layer.py:174) as an operator;
+ComplexityModel keeps hipBLASLt's GEMM with beta = 1 for it, which ran the 1B forward
+0.8% faster.
 """
 
 from __future__ import annotations

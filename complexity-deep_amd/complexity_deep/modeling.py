@@ -10,7 +10,7 @@ The forward (modeling.py:155-219) runs the hot path on the gfx950 kernels:
   * every routed layer gets its own routing plan through its own expert map, all of
     them computed by one call (cdx_route_plans) at the top of the forward;
   * both residual adds of every block run inside the kernels that produce the
-    branch outputs (o_proj's epilogue, cdx_linear_residual_fwd; the MoE down pass's
+    branch outputs (o_proj as hipBLASLt's GEMM with beta = 1, the MoE down pass's
     scatter epilogue), and every norm (each layer's two, the final one) is a
     plain RMSNorm of h;
   * the mu-QKV projection carries QK-norm and RoPE in its epilogue and feeds the

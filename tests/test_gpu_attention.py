@@ -101,9 +101,8 @@ def test_attention_module_matches_sdpa_path(cdx, monkeypatch, H, nq, nkv, S):
 
 def test_attention_residual_out_projection(cdx):
     """ComplexityAttention with ``residual``: o_proj and the block's residual add
-    (core/layer.py:174) as one kernel (cdx_linear_residual_fwd), written into the
-    residual, against the module's nn.Linear o_proj followed by the bf16 add (a
-    different GEMM's accumulation order, so bf16 tolerance)."""
+    (core/layer.py:174) as one GEMM with beta = 1, written into the residual, against
+    o_proj followed by the bf16 add (one rounding fewer, so bf16 tolerance)."""
     print("attention residual o_proj", flush=True)
     torch.manual_seed(11)
     H, nq, nkv, S = 1024, 8, 4, 130
