@@ -127,6 +127,26 @@ def test_cfg1_readme_model_forward(cdx, oracle):
     _check_layers(m, cfg, ids.cuda(), oracle, "cfg1")
 
 
+@pytest.mark.parametrize("B,S", [(3, 333), (1, 1000), (5, 17)])
+def test_ragged_readme_model_forward(cdx, oracle, B, S):
+    """The README model on token counts that fill no tile: sequences that are not a
+    multiple of 16, 64 or 128 tokens (waves whose rows span two sequences, the
+    element-wise V^T stores, partial key tiles, partial M tiles of every GEMM and
+    expert segments of any length), logits and every block's pieces against the
+    oracle at the north-star bound."""
+    from complexity_deep import synthetic as syn
+    print(f"README model ragged B={B} S={S}", flush=True)
+    cfg = readme_config(cdx)
+    m = _build(cdx, cfg, seed=2)
+    ids = syn.zipf_token_ids(B, S, cfg.vocab_size, seed=B * 1000 + S)
+    with torch.no_grad():
+        logits = m(ids.cuda()).logits.float().cpu()
+        ref = oracle.forward(_fp32_state(m), cfg.to_dict(), ids)
+    assert logits.shape == (B, S, cfg.vocab_size)
+    _check(logits, ref, f"ragged {B}x{S} logits")
+    _check_layers(m, cfg, ids.cuda(), oracle, f"ragged {B}x{S}")
+
+
 def test_cfg4_1b_forward(cdx, oracle):
     from complexity_deep import synthetic as syn
     print("cfg4 1B model, 8 x 2048 (sequences 0 and 7 checked)", flush=True)
