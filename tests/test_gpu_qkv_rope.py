@@ -16,7 +16,9 @@ Covered:
   for the CPU chain, since the kernel treats every row independently.
 
 The model path (ComplexityAttention.forward) is checked against the unfused
-projection + PyTorch ops path of the same module.
+projection + PyTorch ops path of the same module, and a cached decode step against the
+behaviour of the reference's SDPA call (top-left causal alignment: the new token sees
+key 0 only).
 """
 
 from __future__ import annotations
@@ -152,6 +154,29 @@ def test_attention_fused_matches_unfused_path(cdx, monkeypatch, H, nq, nkv, with
     d = (fused.float() - unfused.float()).abs().max() / unfused.float().abs().max()
     print("max rel fused vs unfused", float(d), flush=True)
     assert float(d) < 3e-2
+
+
+def test_cached_decode_step_keeps_the_reference_sdpa_alignment(cdx):
+    """A decode step with the KV cache calls SDPA as the reference does
+    (core/attention.py:168-175: is_causal=(attention_mask is None)) with one query
+    against all cached keys.  SDPA aligns a non-square causal mask at the top left, so
+    that query sees key 0 only (the reference's generate() inherits this); the module
+    keeps the call, so with o_proj the identity its output is, per query head, the
+    first value row of that head's KV head, exactly."""
+    H, nq, nkv, D = 256, 4, 2, 64
+    print(f"cached decode step H={H} heads={nq}/{nkv}", flush=True)
+    torch.manual_seed(5)
+    attn = cdx.ComplexityAttention(H, nq, nkv).to(bf16).cuda().eval()
+    with torch.no_grad():
+        attn.o_proj.weight.copy_(torch.eye(H, dtype=bf16))
+        x = torch.randn(2, 9, H, device="cuda").to(bf16)
+        mu = torch.randn(2, 9, H, device="cuda").clamp(-2, 2).to(bf16)
+        _, kv = attn(x[:, :8], mu_prev=mu[:, :8], use_cache=True)
+        out, kv2 = attn(x[:, 8:], mu_prev=mu[:, 8:], past_key_value=kv, use_cache=True)
+    v0 = kv2[1][:, :, 0, :]                                    # [B, nkv, D]
+    expect = v0.repeat_interleave(nq // nkv, dim=1).reshape(2, 1, nq * D)
+    assert kv2[1].shape == (2, nkv, 9, D)
+    assert torch.equal(out, expect)
 
 
 @pytest.mark.parametrize("B,S,H,nq,nkv,mu_mode,pos0,qk_norm", [
