@@ -89,6 +89,9 @@ def work_of(name: str, s: dict):
     if name == "mu_qkv":
         K = 2 * s["H"] if s["mu"] else s["H"]
         return 2.0 * s["M"] * K * s["N"], "flop"
+    if name == "mu_qkv_bcast":
+        # layer 0: the broadcast mu row's product folded into one 64-column K block
+        return 2.0 * s["M"] * (s["H"] + 64) * s["N"], "flop"
     if name == "moe_swiglu":
         blocks = 2 if s["shared"] else 1
         # gate + up + down per block, each token sees one routed expert (+ shared)

@@ -49,6 +49,9 @@ _SIGNATURES = {
     "cdx_mu_qkv_rope_fwd": (ctypes.c_int, [_vp, _i64, _vp, _i64, _vp, _vp, _i64, _i64, _i64, _i32, _i32,
                                            _i32, _i32, _vp, _vp, ctypes.c_float, _vp, _i64, _i64, _vp, _vp,
                                            _vp, _i64, _vp]),
+    "cdx_mu_qkv_rope_bcast_fwd": (ctypes.c_int, [_vp, _i64, _vp, _vp, _vp, _i64, _i64, _i64, _i32, _i32,
+                                                 _i32, _i32, _vp, _vp, ctypes.c_float, _vp, _i64, _i64, _vp,
+                                                 _vp, _vp, _i64, _vp, _vp]),
     "cdx_attention_fwd": (ctypes.c_int, [_vp, _vp, _vp, _i64, _i64, _i32, _i32, _i32, _i64, ctypes.c_float,
                                          _vp, _vp]),
     "cdx_mu_guidance_fwd": (ctypes.c_int, [_vp, _i64, _i32, _vp, _vp, ctypes.c_float, ctypes.c_float,

@@ -140,7 +140,9 @@ def mu_qkv_rope(x: torch.Tensor, mu: Optional[torch.Tensor], w_pack: torch.Tenso
     k_norm_w, None = no norm) and RoPE at positions pos0 .. pos0+S-1 fused into one
     kernel.  cos_sin is the fp32 [n_pos, hd/2, 2] table of RotaryEmbedding.  Weights
     as in mu_qkv_project.  v_transposed=True returns V in the layout of to_vt_layout
-    instead."""
+    instead.  A mu that is one row broadcast to every token (layer 0's mu_init.expand)
+    goes through cdx_mu_qkv_rope_bcast_fwd, which folds its product with W_mu into one
+    64-column K block (K = H + 64 instead of 2H)."""
     nat.require_device(x, mu, w_pack, w_mu, q_norm_w, k_norm_w, what="mu_qkv_rope")
     B, S, _ = x.shape
     x2, ldx = _rows_view(x, H)
@@ -172,7 +174,19 @@ def mu_qkv_rope(x: torch.Tensor, mu: Optional[torch.Tensor], w_pack: torch.Tenso
     else:
         vt_ld = 0
         v = torch.empty(B, nkv, S, hd, dtype=x.dtype, device=x.device)
-    with nat.launch_region("mu_qkv", x.device, M=B * S, H=H, N=(nq + 2 * nkv) * hd, mu=mu2 is not None):
+    N = (nq + 2 * nkv) * hd
+    if mu2 is not None and ldmu == 0 and H > 64:
+        # One broadcast mu row (layer 0's mu_init.expand): its product with W_mu is one
+        # row, folded into a 64-column K block (K = H + 64 instead of 2H).
+        work = torch.empty(N * ldw + 64, dtype=x.dtype, device=x.device)
+        with nat.launch_region("mu_qkv_bcast", x.device, M=B * S, H=H, N=N):
+            nat.check(nat.lib().cdx_mu_qkv_rope_bcast_fwd(
+                x2.data_ptr(), ldx, mu2.data_ptr(), wx_ptr, wmu_ptr, ldw, B, S, H, nq, nkv, hd,
+                nat.ptr(q_norm_w), nat.ptr(k_norm_w), float(eps), cos_sin.data_ptr(), cos_sin.shape[0], pos0,
+                q.data_ptr(), k.data_ptr(), v.data_ptr(), vt_ld, work.data_ptr(), nat.stream_of(x)),
+                "cdx_mu_qkv_rope_bcast_fwd")
+        return q, k, v
+    with nat.launch_region("mu_qkv", x.device, M=B * S, H=H, N=N, mu=mu2 is not None):
         nat.check(nat.lib().cdx_mu_qkv_rope_fwd(
             x2.data_ptr(), ldx, nat.ptr(mu2), ldmu, wx_ptr, wmu_ptr, ldw, B, S, H, nq, nkv, hd,
             nat.ptr(q_norm_w), nat.ptr(k_norm_w), float(eps), cos_sin.data_ptr(), cos_sin.shape[0], pos0,

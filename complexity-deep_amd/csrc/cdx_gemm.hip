@@ -3,6 +3,8 @@
 //                        [W_x | W_mu] (two weight sources, selected by the K half)
 //   cdx_mu_qkv_rope_fwd  the same contraction with QK RMSNorm + RoPE fused into the
 //                        epilogue, writing head-major q, k, v
+//   cdx_mu_qkv_rope_bcast_fwd  the same for one broadcast mu row, its product with
+//                        W_mu folded into a single 64-column K block
 //   cdx_moe_swiglu_fwd   piece 1b: gather + gate/up + SwiGLU, then down + scatter,
 //                        with the shared expert folded into both passes
 //   cdx_moe_swiglu_residual_fwd  the same, the scattered rows added to the residual
@@ -292,56 +294,29 @@ extern "C" int cdx_grouped_gemm_fwd(const uint16_t* a, int64_t T, int32_t K, int
   return launch<ALoad::kDense, Epi::kStore>(p, reinterpret_cast<hipStream_t>(stream), name);
 }
 
-extern "C" int cdx_mu_qkv_rope_fwd(const uint16_t* x, int64_t ldx, const uint16_t* mu, int64_t ldmu,
-                                   const uint16_t* w, const uint16_t* w_mu, int64_t ldw, int64_t B, int64_t S,
-                                   int32_t H,
-                                   int32_t nq, int32_t nkv, int32_t hd, const uint16_t* q_norm_w,
-                                   const uint16_t* k_norm_w, float eps, const float* cos_sin,
-                                   int64_t n_pos, int64_t pos0, uint16_t* q_out, uint16_t* k_out,
-                                   uint16_t* v_out, int64_t vt_ld, void* stream) {
-  using namespace cdx;
-  clear_error();
-  const char* name = "cdx_mu_qkv_rope_fwd";
-  if (B < 0 || S < 0 || H <= 0 || nq <= 0 || nkv <= 0 || pos0 < 0 || n_pos < 0)
-    return fail(CDX_EINVAL, "%s: bad shape B=%lld S=%lld H=%d nq=%d nkv=%d", name, (long long)B, (long long)S,
-                H, nq, nkv);
-  if (hd != 32 && hd != 64 && hd != 128)
-    return fail(CDX_EUNSUPPORTED, "%s: head dim %d must be 32, 64 or 128", name, hd);
-  if (H % 64 != 0) return fail(CDX_EUNSUPPORTED, "%s: H=%d must be a multiple of 64", name, H);
-  if ((q_norm_w == nullptr) != (k_norm_w == nullptr))
-    return fail(CDX_EINVAL, "%s: q and k norm weights must both be given or both be NULL", name);
-  if (!(eps >= 0.f)) return fail(CDX_EINVAL, "%s: eps must be >= 0", name);
+namespace cdx {
+namespace {
+
+// The mu-QKV + QK-norm + RoPE launch shared by both entry points.  A = [x | a2] and
+// B = [w | b2] switch source at K column H; K_total columns in all (2H for a per-token
+// mu, H + 64 for the folded broadcast row, H without a mu term: a2 == NULL).
+int mu_qkv_rope(const char* name, const uint16_t* x, int64_t ldx, const uint16_t* a2, int64_t lda2,
+                const uint16_t* w, const uint16_t* b2, int64_t ldw, int64_t B, int64_t S, int32_t H, int64_t K,
+                int32_t nq, int32_t nkv, int32_t hd, const uint16_t* q_norm_w, const uint16_t* k_norm_w,
+                float eps, const float* cos_sin, int64_t n_pos, int64_t pos0, uint16_t* q_out,
+                uint16_t* k_out, uint16_t* v_out, int64_t vt_ld, void* stream) {
   const int64_t M = B * S;
   const int64_t N = (int64_t)(nq + 2 * nkv) * hd;
-  const int64_t K = mu ? 2 * (int64_t)H : (int64_t)H;
-  if (N > INT32_MAX) return fail(CDX_EUNSUPPORTED, "%s: too many heads", name);
-  if (S > INT32_MAX - 256) return fail(CDX_EUNSUPPORTED, "%s: S=%lld too long", name, (long long)S);
-  if (ldx < H || ldw < H || (mu && ldmu != 0 && ldmu < H))
-    return fail(CDX_EINVAL, "%s: leading dimension too small", name);
-  if (ldx % 8 || ldw % 8 || (mu && ldmu % 8))
-    return fail(CDX_EUNSUPPORTED, "%s: leading dimensions must be multiples of 8", name);
-  if (vt_ld < 0 || (vt_ld > 0 && (vt_ld < S || vt_ld % 64 != 0)))
-    return fail(CDX_EINVAL, "%s: vt_ld=%lld must be 0 or a multiple of 64 that is >= S", name, (long long)vt_ld);
-  if (M == 0) return CDX_OK;
-  if (pos0 + S > n_pos)
-    return fail(CDX_EINVAL, "%s: cos/sin table has %lld positions, needs %lld", name, (long long)n_pos,
-                (long long)(pos0 + S));
-  if (!x || !w || !cos_sin || !q_out || !k_out || !v_out || (mu && !w_mu))
-    return fail(CDX_EINVAL, "%s: null pointer", name);
-  if (!aligned16(x) || !aligned16(w) || !aligned16(cos_sin) || !aligned16(q_out) || !aligned16(k_out) ||
-      !aligned16(v_out) || (mu && (!aligned16(mu) || !aligned16(w_mu))) ||
-      (q_norm_w && (!aligned16(q_norm_w) || !aligned16(k_norm_w))))
-    return fail(CDX_EUNSUPPORTED, "%s: pointers must be 16-byte aligned", name);
   GemmParams p{};
   p.a = x;
   p.lda = ldx;
-  p.a2 = mu;
-  p.lda2 = ldmu;
+  p.a2 = a2;
+  p.lda2 = lda2;
   p.k_split = H;
   p.E = 1;
   p.M = M;
   p.b = w;
-  p.b2 = w_mu;
+  p.b2 = b2;
   p.ldb = ldw;
   p.N = (int32_t)N;
   p.K = (int32_t)K;
@@ -360,17 +335,147 @@ extern "C" int cdx_mu_qkv_rope_fwd(const uint16_t* x, int64_t ldx, const uint16_
   if (cdiv(M, kBM) > INT32_MAX) return fail(CDX_EUNSUPPORTED, "%s: M too large", name);
   p.mt_count = (int32_t)cdiv(M, kBM);
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  const bool concat = a2 != nullptr;
   switch (hd) {
     case 32:
-      return mu ? launch<ALoad::kConcat, Epi::kQKRope, DefaultCfg, 32>(p, st, name)
-                : launch<ALoad::kDense, Epi::kQKRope, DefaultCfg, 32>(p, st, name);
+      return concat ? launch<ALoad::kConcat, Epi::kQKRope, DefaultCfg, 32>(p, st, name)
+                    : launch<ALoad::kDense, Epi::kQKRope, DefaultCfg, 32>(p, st, name);
     case 64:
-      return mu ? launch<ALoad::kConcat, Epi::kQKRope, DefaultCfg, 64>(p, st, name)
-                : launch<ALoad::kDense, Epi::kQKRope, DefaultCfg, 64>(p, st, name);
+      return concat ? launch<ALoad::kConcat, Epi::kQKRope, DefaultCfg, 64>(p, st, name)
+                    : launch<ALoad::kDense, Epi::kQKRope, DefaultCfg, 64>(p, st, name);
     default:
-      return mu ? launch<ALoad::kConcat, Epi::kQKRope, DefaultCfg, 128>(p, st, name)
-                : launch<ALoad::kDense, Epi::kQKRope, DefaultCfg, 128>(p, st, name);
+      return concat ? launch<ALoad::kConcat, Epi::kQKRope, DefaultCfg, 128>(p, st, name)
+                    : launch<ALoad::kDense, Epi::kQKRope, DefaultCfg, 128>(p, st, name);
   }
+}
+
+// Checks shared by both entry points (mu NULL: no mu term; ldmu 0: one broadcast row).
+int check_rope_args(const char* name, const uint16_t* x, int64_t ldx, const uint16_t* mu, int64_t ldmu,
+                    const uint16_t* w, const uint16_t* w_mu, int64_t ldw,
+                    int64_t B, int64_t S, int32_t H, int32_t nq, int32_t nkv, int32_t hd,
+                    const uint16_t* q_norm_w, const uint16_t* k_norm_w, float eps, const float* cos_sin,
+                    int64_t n_pos, int64_t pos0, uint16_t* q_out, uint16_t* k_out, uint16_t* v_out,
+                    int64_t vt_ld) {
+  if (B < 0 || S < 0 || H <= 0 || nq <= 0 || nkv <= 0 || pos0 < 0 || n_pos < 0)
+    return fail(CDX_EINVAL, "%s: bad shape B=%lld S=%lld H=%d nq=%d nkv=%d", name, (long long)B, (long long)S,
+                H, nq, nkv);
+  if (hd != 32 && hd != 64 && hd != 128)
+    return fail(CDX_EUNSUPPORTED, "%s: head dim %d must be 32, 64 or 128", name, hd);
+  if (H % 64 != 0) return fail(CDX_EUNSUPPORTED, "%s: H=%d must be a multiple of 64", name, H);
+  if ((q_norm_w == nullptr) != (k_norm_w == nullptr))
+    return fail(CDX_EINVAL, "%s: q and k norm weights must both be given or both be NULL", name);
+  if (!(eps >= 0.f)) return fail(CDX_EINVAL, "%s: eps must be >= 0", name);
+  if ((int64_t)(nq + 2 * nkv) * hd > INT32_MAX) return fail(CDX_EUNSUPPORTED, "%s: too many heads", name);
+  if (S > INT32_MAX - 256) return fail(CDX_EUNSUPPORTED, "%s: S=%lld too long", name, (long long)S);
+  if (ldx < H || ldw < H || (mu && ldmu != 0 && ldmu < H))
+    return fail(CDX_EINVAL, "%s: leading dimension too small", name);
+  if (ldx % 8 || ldw % 8 || (mu && ldmu % 8))
+    return fail(CDX_EUNSUPPORTED, "%s: leading dimensions must be multiples of 8", name);
+  if (vt_ld < 0 || (vt_ld > 0 && (vt_ld < S || vt_ld % 64 != 0)))
+    return fail(CDX_EINVAL, "%s: vt_ld=%lld must be 0 or a multiple of 64 that is >= S", name, (long long)vt_ld);
+  if (B * S == 0) return CDX_OK;
+  if (pos0 + S > n_pos)
+    return fail(CDX_EINVAL, "%s: cos/sin table has %lld positions, needs %lld", name, (long long)n_pos,
+                (long long)(pos0 + S));
+  if (!x || !w || !cos_sin || !q_out || !k_out || !v_out || (mu && !w_mu))
+    return fail(CDX_EINVAL, "%s: null pointer", name);
+  if (!aligned16(x) || !aligned16(w) || !aligned16(cos_sin) || !aligned16(q_out) || !aligned16(k_out) ||
+      !aligned16(v_out) || (mu && (!aligned16(mu) || !aligned16(w_mu))) ||
+      (q_norm_w && (!aligned16(q_norm_w) || !aligned16(k_norm_w))))
+    return fail(CDX_EUNSUPPORTED, "%s: pointers must be 16-byte aligned", name);
+  return CDX_OK;
+}
+
+// A broadcast mu row (layer 0's mu_init.expand) has one product with W_mu for every
+// token: bias[n] = sum_k mu[k] W_mu[n, k].  This kernel computes it in fp32 (one wave
+// per row n) and writes it as a 64-column K block for the projection: row n of `fold`
+// (row stride ldw, the projection's B stride) gets (hi, lo, 0, ..., 0) with
+// hi = bf16(bias[n]) and lo = bf16(bias[n] - hi), and `unit` (the A row, broadcast)
+// gets (1, 1, 0, ..., 0).  The MFMA adds hi + lo exactly in fp32, which carries the
+// bias to about 2^-17 of its size, so the projection needs one K step for the mu
+// term instead of H / 64.  (A bias that is not finite keeps lo = 0, so that
+// hi + lo is the bias itself.)
+__global__ __launch_bounds__(256) void mu_fold_kernel(const uint16_t* __restrict__ mu,
+                                                      const uint16_t* __restrict__ w, int64_t ldw, int32_t H,
+                                                      int32_t N, uint16_t* __restrict__ fold,
+                                                      uint16_t* __restrict__ unit) {
+  const int lane = threadIdx.x & 63;
+  if (blockIdx.x == 0 && threadIdx.x < 8)
+    *reinterpret_cast<uint4*>(unit + threadIdx.x * 8) =
+        threadIdx.x == 0 ? make_uint4(0x3F803F80u, 0u, 0u, 0u) : make_uint4(0u, 0u, 0u, 0u);
+  const int n = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (n >= N) return;
+  const uint16_t* row = w + (int64_t)n * ldw;
+  float acc = 0.f;
+  for (int k = lane * 8; k < H; k += 64 * 8) {
+    float a[8], b[8];
+    unpack8(*reinterpret_cast<const uint4*>(row + k), a);
+    unpack8(*reinterpret_cast<const uint4*>(mu + k), b);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) acc = __builtin_fmaf(a[i], b[i], acc);
+  }
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) acc += __shfl_xor(acc, off, 64);
+  if (lane < 8) {
+    uint4 v = make_uint4(0u, 0u, 0u, 0u);
+    if (lane == 0) {
+      const uint16_t hi = f32_to_bf16_bits(acc);
+      const float rest = acc - bf16_bits_to_f32(hi);
+      const uint16_t lo = __builtin_isfinite(rest) ? f32_to_bf16_bits(rest) : (uint16_t)0;
+      v.x = (uint32_t)hi | ((uint32_t)lo << 16);
+    }
+    *reinterpret_cast<uint4*>(fold + (int64_t)n * ldw + lane * 8) = v;
+  }
+}
+
+}  // namespace
+}  // namespace cdx
+
+extern "C" int cdx_mu_qkv_rope_fwd(const uint16_t* x, int64_t ldx, const uint16_t* mu, int64_t ldmu,
+                                   const uint16_t* w, const uint16_t* w_mu, int64_t ldw, int64_t B, int64_t S,
+                                   int32_t H,
+                                   int32_t nq, int32_t nkv, int32_t hd, const uint16_t* q_norm_w,
+                                   const uint16_t* k_norm_w, float eps, const float* cos_sin,
+                                   int64_t n_pos, int64_t pos0, uint16_t* q_out, uint16_t* k_out,
+                                   uint16_t* v_out, int64_t vt_ld, void* stream) {
+  using namespace cdx;
+  clear_error();
+  const char* name = "cdx_mu_qkv_rope_fwd";
+  const int rc = check_rope_args(name, x, ldx, mu, ldmu, w, w_mu, ldw, B, S, H, nq, nkv, hd, q_norm_w, k_norm_w,
+                                 eps, cos_sin, n_pos, pos0, q_out, k_out, v_out, vt_ld);
+  if (rc != CDX_OK || B * S == 0) return rc;
+  const int64_t K = mu ? 2 * (int64_t)H : (int64_t)H;
+  return mu_qkv_rope(name, x, ldx, mu, ldmu, w, mu ? w_mu : nullptr, ldw, B, S, H, K, nq, nkv, hd, q_norm_w,
+                     k_norm_w, eps, cos_sin, n_pos, pos0, q_out, k_out, v_out, vt_ld, stream);
+}
+
+extern "C" int cdx_mu_qkv_rope_bcast_fwd(const uint16_t* x, int64_t ldx, const uint16_t* mu_row,
+                                         const uint16_t* w, const uint16_t* w_mu, int64_t ldw, int64_t B,
+                                         int64_t S, int32_t H, int32_t nq, int32_t nkv, int32_t hd,
+                                         const uint16_t* q_norm_w, const uint16_t* k_norm_w, float eps,
+                                         const float* cos_sin, int64_t n_pos, int64_t pos0, uint16_t* q_out,
+                                         uint16_t* k_out, uint16_t* v_out, int64_t vt_ld, uint16_t* work,
+                                         void* stream) {
+  using namespace cdx;
+  clear_error();
+  const char* name = "cdx_mu_qkv_rope_bcast_fwd";
+  if (!mu_row) return fail(CDX_EINVAL, "%s: null pointer", name);
+  int rc = check_rope_args(name, x, ldx, mu_row, 0, w, w_mu, ldw, B, S, H, nq, nkv, hd, q_norm_w, k_norm_w, eps,
+                           cos_sin, n_pos, pos0, q_out, k_out, v_out, vt_ld);
+  if (rc != CDX_OK || B * S == 0) return rc;
+  if (!work) return fail(CDX_EINVAL, "%s: null pointer", name);
+  if (!aligned16(work)) return fail(CDX_EUNSUPPORTED, "%s: pointers must be 16-byte aligned", name);
+  const int32_t N = (nq + 2 * nkv) * hd;
+  // work: the fold block, N rows of stride ldw (64 columns of each written), then the
+  // 64-value unit row.
+  uint16_t* fold = work;
+  uint16_t* unit = work + (int64_t)N * ldw;
+  hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  mu_fold_kernel<<<dim3((unsigned)((N + 3) / 4)), dim3(256), 0, st>>>(mu_row, w_mu, ldw, H, N, fold, unit);
+  rc = check_launch(name);
+  if (rc != CDX_OK) return rc;
+  return mu_qkv_rope(name, x, ldx, unit, 0, w, fold, ldw, B, S, H, (int64_t)H + 64, nq, nkv, hd, q_norm_w,
+                     k_norm_w, eps, cos_sin, n_pos, pos0, q_out, k_out, v_out, vt_ld, stream);
 }
 
 extern "C" int cdx_mu_guidance_fwd(const uint16_t* h, int64_t T, int32_t H, const uint16_t* w,

@@ -277,6 +277,31 @@ int cdx_mu_qkv_rope_fwd(const uint16_t* x_dev, int64_t ldx, const uint16_t* mu_d
                         uint16_t* v_out_dev, int64_t vt_ld, void* stream);
 
 /*
+ * cdx_mu_qkv_rope_fwd for a mu operand that is one row broadcast to every token
+ * (layer 0's mu_init.expand, i.e. ldmu == 0), with the mu term folded:
+ *   bias[n] = sum_k mu_row[k] w_mu[n, k]      (fp32, once per call)
+ *   [q | k | v] = x @ w_x^T + bias            (then QK-norm + RoPE as cdx_mu_qkv_rope_fwd)
+ * The bias enters the contraction as one 64-column K block whose row n holds
+ * (bf16(bias[n]), bf16(bias[n] - bf16(bias[n])), 0, ...), so the product runs
+ * K = H + 64 instead of 2H; hi + lo carries the fp32 bias to about 2^-17 of its
+ * size and everything else is rounded as in cdx_mu_qkv_rope_fwd.
+ *   mu_row  [H] bf16;  w_x / w_mu / ldw and the other arguments as cdx_mu_qkv_rope_fwd.
+ *   work    device scratch of N * ldw + 64 bf16 (N = (nq + 2 nkv) hd), 16-byte
+ *           aligned: the fold block (64 columns of each row written) and its unit A
+ *           row.  Written on every call; calls that share it on one stream are ordered.
+ *
+ * Replaces: core/attention.py:120-155 for layer 0, whose mu_prev is
+ * models/modeling.py:182 (mu_init.expand(B, S, -1)).
+ */
+int cdx_mu_qkv_rope_bcast_fwd(const uint16_t* x_dev, int64_t ldx, const uint16_t* mu_row_dev,
+                              const uint16_t* w_x_dev, const uint16_t* w_mu_dev, int64_t ldw, int64_t B,
+                              int64_t S, int32_t H, int32_t nq, int32_t nkv, int32_t hd,
+                              const uint16_t* q_norm_w_dev, const uint16_t* k_norm_w_dev, float eps,
+                              const float* cos_sin_dev, int64_t n_pos, int64_t pos0, uint16_t* q_out_dev,
+                              uint16_t* k_out_dev, uint16_t* v_out_dev, int64_t vt_ld, uint16_t* work_dev,
+                              void* stream);
+
+/*
  * mu guidance, the producer of the next layer's mu operand:
  *   out[t, n] = clamp(sum_k h[t, k] w[n, k] + clamp(mu[n], mu_lo, mu_hi), lo, hi)
  * h [T, H] bf16, w [H, H] bf16 (nn.Linear layout, [out, in]), mu [H] bf16 (the

@@ -260,3 +260,92 @@ def test_qkv_rope_sequences_independent_of_batch(cdx, B, S, H, nq, nkv):
     torch.cuda.synchronize()
     assert torch.equal(q2, q[:2]) and torch.equal(k2, k[:2])
     assert torch.equal(vt2[..., :S], vt[:2, ..., :S])
+
+
+def _rope_unfolded(x, mu_row, w_pack, H, nq, nkv, D, qn, kn, table, vt):
+    """cdx_mu_qkv_rope_fwd called directly with the broadcast row (ldmu = 0): the full
+    K = 2H contraction that the fold replaces."""
+    from complexity_deep import _native as nat
+    from complexity_deep.attention import vt_ld_for
+    B, S, _ = x.shape
+    q = torch.empty(B, nq, S, D, dtype=bf16, device="cuda")
+    k = torch.empty(B, nkv, S, D, dtype=bf16, device="cuda")
+    vt_ld = vt_ld_for(S) if vt else 0
+    v = torch.zeros(B, nkv, D, vt_ld, dtype=bf16, device="cuda") if vt else torch.empty(B, nkv, S, D, dtype=bf16,
+                                                                                         device="cuda")
+    nat.check(nat.lib().cdx_mu_qkv_rope_fwd(
+        x.data_ptr(), H, mu_row.data_ptr(), 0, w_pack.data_ptr(), w_pack.data_ptr() + 2 * H, 2 * H, B, S, H, nq,
+        nkv, D, qn.data_ptr(), kn.data_ptr(), 1e-6, table.data_ptr(), table.shape[0], 0, q.data_ptr(),
+        k.data_ptr(), v.data_ptr(), vt_ld, nat.stream_of(x)), "cdx_mu_qkv_rope_fwd")
+    return q, k, v
+
+
+@pytest.mark.parametrize("B,S,H,nq,nkv,vt", [
+    (8, 1024, 2048, 16, 8, True),   # 1B layer 0 heads, 512 tiles: the persistent form, K = 2112
+    (2, 256, 768, 12, 4, False),    # README size, D = 64
+    (1, 77, 128, 4, 2, False),      # D = 32, ragged, K = 192 against 256
+])
+def test_broadcast_mu_fold(cdx, oracle, B, S, H, nq, nkv, vt):
+    """Layer 0's broadcast mu row through cdx_mu_qkv_rope_bcast_fwd (its W_mu product
+    folded into one 64-column K block) against the unfolded K = 2H contraction of the
+    same entry point family:
+    * mu = 0: the fold adds exact zeros, so q, k, v equal the no-mu (K = H) kernel's bits;
+    * mu one-hot at column j: the bias is W_mu[:, j] exactly (lo = 0) and the unfolded
+      contraction adds exactly that product to the same fp32 sums, so the bits agree;
+      a fold row or column taken from the wrong place fails here;
+    * random mu: both within 1 bf16 ulp of each other, plus 2^-14 of the tensor's
+      largest magnitude for outputs that RoPE's subtraction brings near zero (the
+      bias's fp32 sum order differs, by a few fp32 ulps of the pre-norm values), and at
+      the bf16 tolerance of the fp32 oracle chain."""
+    from complexity_deep.attention import mu_qkv_rope
+    from complexity_deep.rotary import RotaryEmbedding
+    D = H // nq
+    print(f"broadcast mu fold B={B} S={S} H={H} heads={nq}/{nkv} D={D} vt={vt}", flush=True)
+    g = torch.Generator().manual_seed(B * S + H)
+    x = torch.randn(B, S, H, generator=g).to(bf16)
+    ws = [(torch.randn(d, H, generator=g) * 0.02).to(bf16) for d in (nq * D, nkv * D, nkv * D) * 2]
+    qn = (1 + 0.1 * torch.randn(D, generator=g)).to(bf16).cuda()
+    kn = (1 + 0.1 * torch.randn(D, generator=g)).to(bf16).cuda()
+    rot = RotaryEmbedding(D).cuda()
+    table = rot.cos_sin_table(S, torch.device("cuda"))
+    w_pack = torch.cat([torch.cat(ws[:3], 0), torch.cat(ws[3:], 0)], 1).contiguous().cuda()
+    xd = x.cuda()
+
+    def folded(mu_row):
+        return mu_qkv_rope(xd, mu_row.expand(B, S, H), w_pack, H, nq, nkv, D, qn, kn, 1e-6, table, 0,
+                           v_transposed=vt)
+
+    zero = torch.zeros(1, 1, H, dtype=bf16, device="cuda")
+    no_mu = mu_qkv_rope(xd, None, w_pack, H, nq, nkv, D, qn, kn, 1e-6, table, 0, v_transposed=vt)
+    for a, b, what in zip(folded(zero), no_mu, "qkv"):
+        assert torch.equal(a, b), f"mu = 0: {what} differs from the no-mu kernel"
+
+    j = H // 3
+    one_hot = torch.zeros(1, 1, H, dtype=bf16, device="cuda")
+    one_hot[..., j] = 1.0
+    for a, b, what in zip(folded(one_hot), _rope_unfolded(xd, one_hot, w_pack, H, nq, nkv, D, qn, kn, table, vt),
+                          "qkv"):
+        if vt:
+            a, b = a[..., :S], b[..., :S]
+        assert torch.equal(a, b), f"one-hot mu: {what} differs from the unfolded contraction"
+
+    mu_row = (torch.randn(1, 1, H, generator=g) * 0.5).to(bf16)
+    got = folded(mu_row.cuda())
+    ref = _rope_unfolded(xd, mu_row.cuda(), w_pack, H, nq, nkv, D, qn, kn, table, vt)
+    torch.cuda.synchronize()
+    for a, b, what in zip(got, ref, "qkv"):
+        if vt:
+            a, b = a[..., :S], b[..., :S]
+        a, b = a.float(), b.float()
+        ulp = torch.where(b == 0, torch.zeros_like(b), 2.0 ** (torch.floor(torch.log2(b.abs())) - 7))
+        excess = float(((a - b).abs() - ulp - 2.0 ** -14 * b.abs().max()).max())
+        assert excess <= 0, f"random mu: {what} off the unfolded contraction by {excess:.3g} beyond the bound"
+        assert float((a != b).float().mean()) < 0.01, f"random mu: {what} differs in too many elements"
+    if vt:
+        from complexity_deep.attention import vt_columns
+        got = (got[0], got[1], got[2][..., vt_columns(S, got[2].device)].transpose(-1, -2))
+    rq, rk, rv = _reference(oracle, x[:1], mu_row.expand(1, S, H), ws, nq, nkv, D, qn.cpu(), kn.cpu(),
+                            rot.inv_freq.cpu(), 0)
+    assert_close_bf16(got[0][:1], rq, "q")
+    assert_close_bf16(got[1][:1], rk, "k")
+    assert_close_bf16(got[2][:1], rv, "v")
