@@ -94,6 +94,7 @@ def _case(cdx, oracle, B, S, H, nq, nkv, mu_mode, pos0, qk_norm, seed):
     (1, 100, 256, 2, 1, None, 0, True),            # no mu (K = H), D = 128
     (2, 33, 512, 8, 2, "full", 40, True),          # KV-cache offset
     (4, 1, 512, 8, 8, "full", 511, True),          # decode step
+    (2, 1, 512, 8, 4, "broadcast", 100, True),     # layer 0's decode step (folded broadcast mu)
     (2, 130, 512, 4, 4, "full", 0, False),         # no QK norm
 ])
 def test_qkv_rope_matches_oracle(cdx, oracle, B, S, H, nq, nkv, mu_mode, pos0, qk_norm):
