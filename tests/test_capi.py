@@ -133,6 +133,47 @@ def test_gemm_validation(lib):
     assert lib.cdx_linear_residual_fwd(None, 64, None, 64, 0, 64, 32, None, 32, None) == 0  # M = 0
 
 
+def test_qkv_rope_validation(lib):
+    # (x, ldx, mu, ldmu, w, w_mu, ldw, B, S, H, nq, nkv, hd, qn, kn, eps, cos_sin, n_pos, pos0, q, k, v, vt_ld)
+    ok = [16, 128, 16, 128, 16, 16, 128, 1, 4, 128, 2, 1, 64, None, None, 1e-6, 16, 4, 0, 16, 16, 16, 0]
+
+    def rope(**kw):
+        args = list(ok)
+        names = ["x", "ldx", "mu", "ldmu", "w", "w_mu", "ldw", "B", "S", "H", "nq", "nkv", "hd", "qn", "kn", "eps",
+                 "cos_sin", "n_pos", "pos0", "q", "k", "v", "vt_ld"]
+        for key, val in kw.items():
+            args[names.index(key)] = val
+        return lib.cdx_mu_qkv_rope_fwd(*args, None)
+
+    assert rope(hd=48, B=0) == CDX_EUNSUPPORTED
+    assert rope(ldmu=64, B=0) == CDX_EINVAL                      # mu rows shorter than H
+    assert rope(qn=16, B=0) == CDX_EINVAL                        # one QK norm weight only
+    assert rope(vt_ld=65, B=0) == CDX_EINVAL
+    assert rope(n_pos=3) == CDX_EINVAL                           # table shorter than pos0 + S
+    assert rope(w_mu=None) == CDX_EINVAL                         # mu without its weights
+    assert rope(B=0) == 0                                        # no rows: nothing to do
+
+    # (x, ldx, mu_row, w, w_mu, ldw, B, S, H, nq, nkv, hd, qn, kn, eps, cos_sin, n_pos, pos0, q, k, v, vt_ld, work)
+    bc = [16, 128, 16, 16, 16, 128, 1, 4, 128, 2, 1, 64, None, None, 1e-6, 16, 4, 0, 16, 16, 16, 0, 16]
+
+    def bcast(**kw):
+        args = list(bc)
+        names = ["x", "ldx", "mu_row", "w", "w_mu", "ldw", "B", "S", "H", "nq", "nkv", "hd", "qn", "kn", "eps",
+                 "cos_sin", "n_pos", "pos0", "q", "k", "v", "vt_ld", "work"]
+        for key, val in kw.items():
+            args[names.index(key)] = val
+        return lib.cdx_mu_qkv_rope_bcast_fwd(*args, None)
+
+    assert bcast(mu_row=None) == CDX_EINVAL
+    assert bcast(work=None) == CDX_EINVAL                        # the fold needs its scratch
+    assert bcast(work=24) == CDX_EUNSUPPORTED                    # scratch not 16-byte aligned
+    assert bcast(ldw=132) == CDX_EUNSUPPORTED                    # B stride not a multiple of 8
+    assert bcast(w_mu=None) == CDX_EINVAL
+    assert bcast(H=96) == CDX_EUNSUPPORTED
+    assert b"cdx_mu_qkv_rope_bcast_fwd" in lib.cdx_last_error()
+    assert bcast(B=0, work=None) == 0                            # no rows: nothing to do
+
+
 def test_cpu_tensors_raise():
     from complexity_deep.normalization import add_rms_norm
     x = torch.randn(4, 64, dtype=torch.bfloat16)
