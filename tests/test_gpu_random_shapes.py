@@ -13,7 +13,8 @@ References, on the same bf16 inputs:
     in torch on the GPU;
   * the MoE: oracle.token_routed_mlp (fp32, pinned by a per-token brute force);
   * attention: oracle.causal_attention (fp32, pinned by SDPA);
-  * the add + RMSNorm: oracle.add_rms_norm, and the bf16 add bit for bit.
+  * the add + RMSNorm: oracle.add_rms_norm, and the bf16 add bit for bit;
+  * layer 0's folded projection (a broadcast mu row): the unfolded K = 2H contraction.
 Bound: the bf16 tolerance of the north star (max rel err <= 2e-2 normwise, mean abs err
 <= 1e-3 against the fp32 reference rounded to bf16), checked by ``assert_close_bf16``.
 """
@@ -173,3 +174,69 @@ def test_random_add_rmsnorm(cdx, oracle, case):
     assert torch.equal(h.cpu(), h_ref), f"bf16 add T={T} H={H}"
     y_ref, _ = oracle.add_rms_norm(h_ref.float(), torch.zeros(T, H), w.float(), 1e-6)
     assert_close_bf16(y, y_ref, f"add_rmsnorm T={T} H={H}")
+
+
+def _rope_unfolded(x, mu_row, w_pack, H, nq, nkv, D, qn, kn, table, pos0, vt):
+    """cdx_mu_qkv_rope_fwd with the broadcast row at ldmu = 0: the K = 2H contraction."""
+    from complexity_deep import _native as nat
+    from complexity_deep.attention import vt_ld_for
+    B, S, _ = x.shape
+    q = torch.empty(B, nq, S, D, dtype=bf16, device="cuda")
+    k = torch.empty(B, nkv, S, D, dtype=bf16, device="cuda")
+    vt_ld = vt_ld_for(S) if vt else 0
+    v = torch.zeros(B, nkv, D, vt_ld, dtype=bf16, device="cuda") if vt else torch.empty(B, nkv, S, D, dtype=bf16,
+                                                                                         device="cuda")
+    nat.check(nat.lib().cdx_mu_qkv_rope_fwd(
+        x.data_ptr(), H, mu_row.data_ptr(), 0, w_pack.data_ptr(), w_pack.data_ptr() + 2 * H, 2 * H, B, S, H, nq,
+        nkv, D, nat.ptr(qn), nat.ptr(kn), 1e-6, table.data_ptr(), table.shape[0], pos0, q.data_ptr(),
+        k.data_ptr(), v.data_ptr(), vt_ld, nat.stream_of(x)), "cdx_mu_qkv_rope_fwd")
+    return q, k, v
+
+
+@pytest.mark.parametrize("case", range(8))
+def test_random_broadcast_mu_fold(cdx, case):
+    """Layer 0's folded projection (cdx_mu_qkv_rope_bcast_fwd, through mu_qkv_rope with a
+    broadcast row) against the unfolded K = 2H contraction on random shapes: bit for bit
+    for a one-hot mu row (the bias is then one column of W_mu exactly), within 1 bf16
+    ulp plus 2^-14 of the largest output for a random row (the bias's fp32 summation
+    order differs)."""
+    from complexity_deep.attention import mu_qkv_rope
+    from complexity_deep.rotary import RotaryEmbedding
+    rng = random.Random(7000 + case)
+    D = rng.choice([32, 64, 128])
+    nkv = rng.choice([1, 2, 4])
+    nq = nkv * rng.choice([1, 2, 4])
+    while nq * D <= 64 or (nq * D) % 64:
+        nq *= 2
+    H = nq * D
+    B = rng.randint(1, 4)
+    S = _log_int(rng, 1, 600)
+    pos0 = rng.choice([0, 0, rng.randint(1, 50)])
+    vt = pos0 == 0 and rng.random() < 0.5
+    qk_norm = rng.random() < 0.8
+    print(f"broadcast fold case {case}: B={B} S={S} H={H} heads={nq}/{nkv} D={D} pos0={pos0} vt={vt} "
+          f"qk_norm={qk_norm}", flush=True)
+    g = torch.Generator().manual_seed(case)
+    x = torch.randn(B, S, H, generator=g).to(bf16).cuda()
+    N = (nq + 2 * nkv) * D
+    w_pack = (torch.randn(N, 2 * H, generator=g) * H ** -0.5).to(bf16).cuda()
+    qn = (1 + 0.1 * torch.randn(D, generator=g)).to(bf16).cuda() if qk_norm else None
+    kn = (1 + 0.1 * torch.randn(D, generator=g)).to(bf16).cuda() if qk_norm else None
+    table = RotaryEmbedding(D).cuda().cos_sin_table(pos0 + S, torch.device("cuda"))
+
+    def both(mu_row):
+        a = mu_qkv_rope(x, mu_row.expand(B, S, H), w_pack, H, nq, nkv, D, qn, kn, 1e-6, table, pos0, v_transposed=vt)
+        b = _rope_unfolded(x, mu_row, w_pack, H, nq, nkv, D, qn, kn, table, pos0, vt)
+        # (V^T buffers: both hold zeros in every column no token maps to)
+        return list(zip(a, b))
+
+    one_hot = torch.zeros(1, 1, H, dtype=bf16, device="cuda")
+    one_hot[..., rng.randrange(H)] = rng.choice([1.0, -2.0, 0.5])
+    for (a, b), what in zip(both(one_hot), "qkv"):
+        assert torch.equal(a, b), f"one-hot mu: {what} differs from the unfolded contraction"
+    mu_row = torch.randn(1, 1, H, generator=g).clamp(-2, 2).to(bf16).cuda()
+    for (a, b), what in zip(both(mu_row), "qkv"):
+        a, b = a.float(), b.float()
+        ulp = torch.where(b == 0, torch.zeros_like(b), 2.0 ** (torch.floor(torch.log2(b.abs())) - 7))
+        excess = float(((a - b).abs() - ulp - 2.0 ** -14 * b.abs().max()).max())
+        assert excess <= 0, f"random mu: {what} off the unfolded contraction by {excess:.3g} beyond the bound"
