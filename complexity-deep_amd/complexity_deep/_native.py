@@ -28,6 +28,7 @@ _SIGNATURES = {
     "cdx_version": (ctypes.c_int, []),
     "cdx_last_error": (ctypes.c_char_p, []),
     "cdx_add_rmsnorm_fwd": (ctypes.c_int, [_vp, _vp, _vp, ctypes.c_float, _i64, _i32, _vp, _vp, _vp]),
+    "cdx_rmsnorm_ld_fwd": (ctypes.c_int, [_vp, _vp, ctypes.c_float, _i64, _i32, _vp, _i64, _vp]),
     "cdx_route_workspace_bytes": (ctypes.c_size_t, [_i64, _i32]),
     "cdx_route_plan": (ctypes.c_int, [_vp, _i64, _vp, _i64, _i32, _vp, _vp, _vp, _vp, _vp, _vp,
                                       ctypes.c_size_t, _vp]),
@@ -55,7 +56,7 @@ _SIGNATURES = {
     "cdx_attention_fwd": (ctypes.c_int, [_vp, _vp, _vp, _i64, _i64, _i32, _i32, _i32, _i64, ctypes.c_float,
                                          _vp, _vp]),
     "cdx_mu_guidance_fwd": (ctypes.c_int, [_vp, _i64, _i32, _vp, _vp, ctypes.c_float, ctypes.c_float,
-                                           ctypes.c_float, ctypes.c_float, _vp, _vp]),
+                                           ctypes.c_float, ctypes.c_float, _vp, _i64, _vp]),
     "cdx_binpack_map": (ctypes.c_int, [_vp, _i64, _i32, _vp]),
     "cdx_embedding_fwd": (ctypes.c_int, [_vp, _i64, _vp, _i64, _i32, _vp, _vp]),
     "cdx_linear_fwd": (ctypes.c_int, [_vp, _i64, _vp, _i64, _i64, _i32, _i32, _vp, _i64, _vp]),
@@ -152,6 +153,26 @@ def stream_of(t: torch.Tensor) -> int:
 
 def ptr(t: Optional[torch.Tensor]) -> Optional[int]:
     return None if t is None else t.data_ptr()
+
+
+def row_stride(t: torch.Tensor, H: int, what: str) -> int:
+    """Row stride (elements) of a [..., H] tensor whose rows are base + r * ld with unit
+    stride inside a row, e.g. a column slice of a wider buffer.  Raises if the rows are
+    not evenly spaced: an output is written in place and cannot be made contiguous."""
+    if t.shape[-1] != H or t.stride(-1) != 1:
+        raise ValueError(f"{what}: rows of {H} elements with unit stride expected, got shape {tuple(t.shape)} "
+                         f"strides {t.stride()}")
+    rows = t.numel() // H if H else 0
+    if t.dim() == 1 or rows <= 1:
+        return H
+    dims = [(n, st) for n, st in zip(t.shape[:-1], t.stride()[:-1]) if n != 1]
+    ld = dims[-1][1]
+    for (n_outer, st_outer), (n_inner, st_inner) in zip(dims, dims[1:]):
+        if st_outer != st_inner * n_inner:
+            raise ValueError(f"{what}: rows are not evenly spaced (strides {t.stride()})")
+    if ld < H:
+        raise ValueError(f"{what}: row stride {ld} is smaller than the row ({H})")
+    return ld
 
 
 def require_device(*tensors: Optional[torch.Tensor], dtype: Optional[torch.dtype] = torch.bfloat16,

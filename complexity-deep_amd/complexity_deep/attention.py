@@ -8,10 +8,13 @@ Interfaces follow the reference:
 
 The projection is one MFMA contraction over K = 2H: [x | mu_prev] @ [W_x | W_mu]^T
 with W_x = [Wq; Wk; Wv] and W_mu = [Wmu_q; Wmu_k; Wmu_v], the kernel switching weight
-source at K = H.  The module keeps W_x and W_mu as two [N, H] buffers and its six
-Linear weights are row views of them, so nothing is concatenated per forward
+source at K = H.  The module keeps W_x and W_mu side by side in one [N, 2H] buffer
+(row n is [W_x[n] | W_mu[n]], the layout of the reference's torch.cat(..., dim=1)) and
+its six Linear weights are views of it, so nothing is concatenated per forward
 (attention.py:122-124 concatenates every call) and every write to a weight, through
-``.data`` or otherwise, reaches the kernel operand.  q, k and v are column slices of
+``.data`` or otherwise, reaches the kernel operand.  When x and mu also sit side by
+side in one [T, 2H] buffer (the model writes them so), the projection is one plain
+K = 2H contraction over single operands.  q, k and v are column slices of
 the packed [T, Nq*D + 2*Nkv*D] output.
 
 ComplexityAttention.forward goes one step further for head dims 32/64/128: the
@@ -175,6 +178,17 @@ def mu_qkv_rope(x: torch.Tensor, mu: Optional[torch.Tensor], w_pack: torch.Tenso
         vt_ld = 0
         v = torch.empty(B, nkv, S, hd, dtype=x.dtype, device=x.device)
     N = (nq + 2 * nkv) * hd
+    esz = x.element_size()
+    if (mu2 is not None and ldmu != 0 and ldx == ldmu and ldx >= 2 * H and ldw >= 2 * H
+            and mu2.data_ptr() == x2.data_ptr() + H * esz and wmu_ptr == wx_ptr + H * esz):
+        # x and mu side by side in one buffer, and W_x and W_mu likewise: one K = 2H
+        # contraction over single operands (the same sums in the same order).
+        with nat.launch_region("mu_qkv", x.device, M=B * S, H=H, N=N, mu=True):
+            nat.check(nat.lib().cdx_mu_qkv_rope_fwd(
+                x2.data_ptr(), ldx, None, 0, wx_ptr, None, ldw, B, S, 2 * H, nq, nkv, hd,
+                nat.ptr(q_norm_w), nat.ptr(k_norm_w), float(eps), cos_sin.data_ptr(), cos_sin.shape[0], pos0,
+                q.data_ptr(), k.data_ptr(), v.data_ptr(), vt_ld, nat.stream_of(x)), "cdx_mu_qkv_rope_fwd")
+        return q, k, v
     if mu2 is not None and ldmu == 0 and H > 64:
         # One broadcast mu row (layer 0's mu_init.expand): its product with W_mu is one
         # row, folded into a 64-column K block (K = H + 64 instead of 2H).
@@ -267,7 +281,9 @@ class FusedMuQKVProjection(nn.Module):
 
 class QKVWeights:
     """The kernel operands W_x = [Wq; Wk; Wv] and W_mu = [Wmu_q; Wmu_k; Wmu_v] of one
-    module, as one [2, N, H] buffer whose rows the six Linear weights are views of.
+    module, side by side in one [N, 2H] buffer (row n = [W_x[n] | W_mu[n]], the
+    reference's torch.cat([q_proj.weight, mu_to_q.weight], dim=1) for each of q, k, v)
+    whose column halves the six Linear weights are views of.
 
     A write to a weight (in place, through ``.data``, by load_state_dict) therefore
     lands in the operand the kernel reads; nothing is cached that could go stale.
@@ -288,7 +304,8 @@ class QKVWeights:
         ws = [lin.weight for lin in self._linears(m)]
         if self.buf is None or [w.data_ptr() for w in ws] != self.ptrs:
             self._bind(ws, m.hidden_size)
-        return self.buf[0], self.buf[1]
+        H = m.hidden_size
+        return self.buf[:, :H], self.buf[:, H:]
 
     def _bind(self, ws, H: int) -> None:
         dt, dev = ws[0].dtype, ws[0].device
@@ -300,14 +317,14 @@ class QKVWeights:
             raise ValueError("ComplexityAttention: mu_to_q/k/v must have the shapes of q/k/v_proj")
         N = sum(w.shape[0] for w in xs)
         with torch.inference_mode(False), torch.no_grad():
-            buf = torch.empty(2, N, H, dtype=dt, device=dev)
+            buf = torch.empty(N, 2 * H, dtype=dt, device=dev)
             r = 0
             for wx, wm in zip(xs, mus):
                 n = wx.shape[0]
-                buf[0, r:r + n].copy_(wx)
-                buf[1, r:r + n].copy_(wm)
-                wx.data = buf[0, r:r + n]
-                wm.data = buf[1, r:r + n]
+                buf[r:r + n, :H].copy_(wx)
+                buf[r:r + n, H:].copy_(wm)
+                wx.data = buf[r:r + n, :H]
+                wm.data = buf[r:r + n, H:]
                 r += n
         self.buf = buf
         self.ptrs = [w.data_ptr() for w in ws]
@@ -348,8 +365,8 @@ class ComplexityAttention(nn.Module):
         self._qkv_w = QKVWeights()
 
     def qkv_weights(self) -> Tuple[torch.Tensor, torch.Tensor]:
-        """(W_x, W_mu), each [Nq*D + 2*Nkv*D, H]: the buffers the six projection weights
-        are views of, i.e. exactly what the kernels read."""
+        """(W_x, W_mu), each [Nq*D + 2*Nkv*D, H]: the two column halves of the [N, 2H]
+        buffer the six projection weights are views of, i.e. exactly what the kernels read."""
         return self._qkv_w.get(self)
 
     def project_qkv(self, hidden_states: torch.Tensor, mu_prev: Optional[torch.Tensor]) -> torch.Tensor:

@@ -27,10 +27,12 @@ from .token_routed_mlp import RoutePlan, TokenRoutedMLP
 
 
 def mu_guidance(h: torch.Tensor, w: torch.Tensor, mu: torch.Tensor, mu_lo: float = -math.inf,
-                mu_hi: float = math.inf, lo: float = -math.inf, hi: float = math.inf) -> torch.Tensor:
+                mu_hi: float = math.inf, lo: float = -math.inf, hi: float = math.inf,
+                out: Optional[torch.Tensor] = None) -> torch.Tensor:
     """clamp(h @ w^T + clamp(mu, mu_lo, mu_hi), lo, hi) through cdx_mu_guidance_fwd (fp32
-    accumulate, one rounding).  h [..., H], w [H, H] and mu [H], all bf16."""
-    nat.require_device(h, w, mu, what="mu_guidance")
+    accumulate, one rounding).  h [..., H], w [H, H] and mu [H], all bf16.  ``out`` may be
+    any [..., H] view with evenly spaced rows (e.g. the right half of a [T, 2H] buffer)."""
+    nat.require_device(h, w, mu, out, what="mu_guidance")
     H = h.shape[-1]
     h2 = h if h.is_contiguous() else h.contiguous()  # rows base + r * H
     T = h2.numel() // H if H else 0
@@ -38,11 +40,15 @@ def mu_guidance(h: torch.Tensor, w: torch.Tensor, mu: torch.Tensor, mu_lo: float
     mu = mu if mu.is_contiguous() else mu.contiguous()
     if mu.shape != (H,):
         raise ValueError(f"mu_guidance: mu must be [{H}], got {tuple(mu.shape)}")
-    out = torch.empty(h.shape, dtype=h.dtype, device=h.device)
+    if out is None:
+        out = torch.empty(h.shape, dtype=h.dtype, device=h.device)
+    elif out.shape != h.shape:
+        raise ValueError(f"mu_guidance: out must have shape {tuple(h.shape)}, got {tuple(out.shape)}")
+    ldo = nat.row_stride(out, H, "mu_guidance out")
     with nat.launch_region("mu_guidance", h.device, T=T, H=H):
         nat.check(nat.lib().cdx_mu_guidance_fwd(h2.data_ptr(), T, H, w.data_ptr(), mu.data_ptr(),
                                                 float(mu_lo), float(mu_hi), float(lo), float(hi), out.data_ptr(),
-                                                nat.stream_of(h)), "cdx_mu_guidance_fwd")
+                                                ldo, nat.stream_of(h)), "cdx_mu_guidance_fwd")
     return out
 
 
@@ -62,9 +68,10 @@ class MuGuidance(nn.Module):
         self.mu_proj = nn.Linear(hidden_size, hidden_size, bias=False)
         nn.init.zeros_(self.mu_proj.weight)
 
-    def fused(self, hidden_states: torch.Tensor, lo: float = -math.inf, hi: float = math.inf) -> torch.Tensor:
+    def fused(self, hidden_states: torch.Tensor, lo: float = -math.inf, hi: float = math.inf,
+              out: Optional[torch.Tensor] = None) -> torch.Tensor:
         forward_only("MuGuidance", hidden_states, module=self)
-        return mu_guidance(hidden_states, self.mu_proj.weight, self.mu, self.mu_min, self.mu_max, lo, hi)
+        return mu_guidance(hidden_states, self.mu_proj.weight, self.mu, self.mu_min, self.mu_max, lo, hi, out=out)
 
     def forward(self, hidden_states: torch.Tensor) -> torch.Tensor:
         return self.fused(hidden_states)
@@ -121,7 +128,7 @@ class TransformerBlock(nn.Module):
     def forward_fused(self, h: torch.Tensor, normed: torch.Tensor, next_norm: RMSNorm,
                       attention_mask=None, past_key_value=None, use_cache: bool = False,
                       token_ids=None, mu_prev=None, route: Optional[RoutePlan] = None,
-                      want_mu: bool = True):
+                      want_mu: bool = True, pair: Optional[torch.Tensor] = None):
         """One block given h (updated in place) and normed = input_layernorm(h).
 
         Returns (h, next_norm(h_out), new_kv, mu) where mu is already clamped to [-2, 2],
@@ -129,7 +136,11 @@ class TransformerBlock(nn.Module):
         (core/layer.py:174, 183) happen inside the kernels that produce the branch
         outputs: o_proj as a GEMM with beta = 1 and the MoE down pass's scatter
         epilogue; the norms that follow read h alone.  ``want_mu=False`` skips mu for
-        the last layer, whose mu the reference computes and then discards."""
+        the last layer, whose mu the reference computes and then discards.  ``pair``, a
+        [..., 2H] buffer, receives next_norm(h_out) in its left half and mu in its right
+        half (the returned tensors are those halves), so that the next layer's projection
+        reads [x | mu] as one operand; the caller reads them before the next call writes
+        the buffer again."""
         if not h.is_contiguous():
             raise ValueError("forward_fused: h must be contiguous (it is updated in place)")
         _, new_kv = self.self_attn(normed, attention_mask=attention_mask, past_key_value=past_key_value,
@@ -137,6 +148,12 @@ class TransformerBlock(nn.Module):
         ln = self.post_attention_layernorm
         normed = rms_norm(h, ln.weight, ln.eps)
         self._mlp(normed, token_ids, route, residual=h)
-        normed = rms_norm(h, next_norm.weight, next_norm.eps)
-        mu = self.mu_guidance.fused(h, -2.0, 2.0) if (want_mu and self.mu_guidance is not None) else None
+        H = h.shape[-1]
+        mu_out = None
+        if pair is not None and want_mu and self.mu_guidance is not None:
+            normed, mu_out = pair[..., :H], pair[..., H:]
+            rms_norm(h, next_norm.weight, next_norm.eps, out=normed)
+        else:
+            normed = rms_norm(h, next_norm.weight, next_norm.eps)
+        mu = self.mu_guidance.fused(h, -2.0, 2.0, out=mu_out) if (want_mu and self.mu_guidance is not None) else None
         return h, normed, new_kv, mu

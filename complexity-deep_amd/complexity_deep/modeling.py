@@ -224,6 +224,10 @@ class ComplexityModel(nn.Module):
         n_layers = len(self.layers)
         normed = rms_norm(h, self.layers[0].input_layernorm.weight, self.layers[0].input_layernorm.eps) \
             if n_layers else rms_norm(h, self.norm.weight, self.norm.eps)
+        # Layers 1.. read their normalised input and mu side by side from one [B, S, 2H]
+        # buffer, written by the layer before (one K = 2H operand for the projection).
+        pair = torch.empty(B, S, 2 * h.shape[-1], dtype=h.dtype, device=h.device) \
+            if self.config.use_mu_guidance and n_layers > 1 else None
         for i, layer in enumerate(self.layers):
             last = i + 1 == n_layers
             next_norm = self.norm if last else self.layers[i + 1].input_layernorm
@@ -231,7 +235,7 @@ class ComplexityModel(nn.Module):
                 h, normed, next_norm, attention_mask=attention_mask,
                 past_key_value=past_key_values[i] if past_key_values is not None else None,
                 use_cache=use_cache, token_ids=input_ids, mu_prev=mu_prev, route=plans[i],
-                want_mu=not last)
+                want_mu=not last, pair=None if last else pair)
             if mu is not None:
                 mu_prev = mu  # clamped to [-2, 2] inside the mu-guidance kernel
             if use_cache:

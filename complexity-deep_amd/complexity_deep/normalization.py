@@ -80,8 +80,28 @@ def add_rms_norm(x: torch.Tensor, residual: Optional[torch.Tensor], weight: torc
     return y, h
 
 
-def rms_norm(x: torch.Tensor, weight: torch.Tensor, eps: float = 1e-6) -> torch.Tensor:
-    return add_rms_norm(x, None, weight, eps)[0]
+def rms_norm(x: torch.Tensor, weight: torch.Tensor, eps: float = 1e-6,
+             out: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """Plain RMSNorm.  ``out`` may be any [..., H] view whose rows are evenly spaced, e.g.
+    the left half of a [T, 2H] buffer (cdx_rmsnorm_ld_fwd writes rows at that stride)."""
+    if out is None or out.is_contiguous():
+        return add_rms_norm(x, None, weight, eps, out=out)[0]
+    forward_only("rms_norm", x, weight)
+    nat.require_device(x, out, what="rms_norm")
+    H = x.shape[-1]
+    if out.shape != x.shape or out.dtype != x.dtype:
+        raise ValueError(f"rms_norm: out must be a {x.dtype} tensor of shape {tuple(x.shape)}, "
+                         f"got {out.dtype} {tuple(out.shape)}")
+    ldo = nat.row_stride(out, H, "rms_norm out")
+    x2 = x if x.is_contiguous() else x.contiguous()
+    T = x2.numel() // H if H else 0
+    w = _weight(weight, x2)
+    if w.numel() != H:
+        raise ValueError(f"rms_norm: weight has {w.numel()} elements, hidden size is {H}")
+    with nat.launch_region("rmsnorm", x.device, T=T, H=H, residual=False, store_residual=False):
+        nat.check(nat.lib().cdx_rmsnorm_ld_fwd(x2.data_ptr(), w.data_ptr(), float(eps), T, H, out.data_ptr(), ldo,
+                                               nat.stream_of(x)), "cdx_rmsnorm_ld_fwd")
+    return out
 
 
 class RMSNorm(nn.Module):

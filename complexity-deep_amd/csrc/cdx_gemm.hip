@@ -74,6 +74,8 @@ int launch(GemmParams p, hipStream_t s, const char* name) {
     return fail(CDX_EUNSUPPORTED, "%s: K=%d must be a positive multiple of %d", name, p.K, Cfg::BK);
   // Whole tiles of a plain (unsegmented) product, the gathered SwiGLU pass with whole
   // N tiles, and mu-QKV with the QK-norm + RoPE epilogue (head dim 128, V transposed,
+  // A from two sources switching at K = H, or from one: x alone, or x and mu side by
+  // side in one [T, 2H] buffer;
   // whole M tiles, sequences a multiple of 128 tokens) run on the persistent form when
   // they have more tiles than CUs: one block per CU (a multiple of 8, so that every
   // XCD's share of the tiles has blocks) walking its XCD's tiles.  (For the gathered
@@ -83,7 +85,7 @@ int launch(GemmParams p, hipStream_t s, const char* name) {
       ((AL == ALoad::kDense || AL == ALoad::kConcat) && (EP == Epi::kStore || EP == Epi::kBiasClamp)) ||
       (AL == ALoad::kDense && EP == Epi::kScatterAdd);
   constexpr bool kGatherTiles = AL == ALoad::kGather && EP == Epi::kSwiGLU;
-  constexpr bool kRopeTiles = AL == ALoad::kConcat && EP == Epi::kQKRope && HD == 128;
+  constexpr bool kRopeTiles = (AL == ALoad::kConcat || AL == ALoad::kDense) && EP == Epi::kQKRope && HD == 128;
   if constexpr ((kDenseTiles || kGatherTiles || kRopeTiles) && Cfg::BN == 256) {
     const int64_t grid = (device_cu_count() + kNumXcd - 1) / kNumXcd * kNumXcd;
     bool whole = kGatherTiles ? p.offsets != nullptr : (p.offsets == nullptr && p.M % kBM == 0);
@@ -480,13 +482,15 @@ extern "C" int cdx_mu_qkv_rope_bcast_fwd(const uint16_t* x, int64_t ldx, const u
 
 extern "C" int cdx_mu_guidance_fwd(const uint16_t* h, int64_t T, int32_t H, const uint16_t* w,
                                    const uint16_t* mu, float mu_lo, float mu_hi, float lo, float hi, uint16_t* out,
-                                   void* stream) {
+                                   int64_t ldo, void* stream) {
   using namespace cdx;
   clear_error();
   const char* name = "cdx_mu_guidance_fwd";
   if (T < 0 || H <= 0) return fail(CDX_EINVAL, "%s: bad shape T=%lld H=%d", name, (long long)T, H);
   if (H % 64 != 0) return fail(CDX_EUNSUPPORTED, "%s: H=%d must be a multiple of 64", name, H);
   if (!(lo <= hi) || !(mu_lo <= mu_hi)) return fail(CDX_EINVAL, "%s: clamp ranges must satisfy lo <= hi", name);
+  if (ldo < H) return fail(CDX_EINVAL, "%s: ldo=%lld is smaller than H=%d", name, (long long)ldo, H);
+  if (ldo % 8 != 0) return fail(CDX_EUNSUPPORTED, "%s: ldo=%lld must be a multiple of 8", name, (long long)ldo);
   if (T == 0) return CDX_OK;
   if (!h || !w || !mu || !out) return fail(CDX_EINVAL, "%s: null pointer", name);
   if (!aligned16(h) || !aligned16(w) || !aligned16(mu) || !aligned16(out))
@@ -502,7 +506,7 @@ extern "C" int cdx_mu_guidance_fwd(const uint16_t* h, int64_t T, int32_t H, cons
   p.N = H;
   p.K = H;
   p.c = out;
-  p.ldc = H;
+  p.ldc = ldo;
   p.bias = mu;
   p.bias_lo = mu_lo;
   p.bias_hi = mu_hi;

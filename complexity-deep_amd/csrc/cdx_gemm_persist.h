@@ -32,9 +32,10 @@ __global__ __launch_bounds__(kGemmThreads, 1) void gemm_persist_kernel(const Gem
   // add fused into a plain product.
   static_assert(((AL == ALoad::kDense || AL == ALoad::kConcat) && (EP == Epi::kStore || EP == Epi::kBiasClamp)) ||
                     (AL == ALoad::kDense && EP == Epi::kScatterAdd) || (kGathered && EP == Epi::kSwiGLU) ||
-                    (AL == ALoad::kConcat && EP == Epi::kQKRope && HD == 128),
+                    ((AL == ALoad::kConcat || AL == ALoad::kDense) && EP == Epi::kQKRope && HD == 128),
                 "persistent tiles: dense/concat A with store or bias-clamp, dense A with the residual add, "
-                "gathered A with SwiGLU, or mu-QKV with the QK-norm + RoPE epilogue at head dim 128");
+                "gathered A with SwiGLU, or mu-QKV (dense or concat A) with the QK-norm + RoPE epilogue at "
+                "head dim 128");
   static_assert(Cfg::STAGES == 2 && Cfg::MINB == 1 && Cfg::BN == 256 && Cfg::BM == kBM,
                 "persistent tiles: 256 x 256, two stages");
   constexpr int kBN = Cfg::BN, kBK = Cfg::BK, kStages = 2;

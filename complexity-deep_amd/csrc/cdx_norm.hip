@@ -13,7 +13,8 @@
 // exactly like the reference's bf16 add, the sum of squares is accumulated in fp32
 // over the rounded h, and the normalised output is rounded to bf16 once.  Traffic
 // per row is the algorithmic minimum: read x, residual (2H bytes each), write h and
-// out.
+// out.  The output rows may sit at a stride wider than H (cdx_rmsnorm_ld_fwd): the
+// model writes the next layer's normalised x beside its mu in one [T, 2H] buffer.
 #include <algorithm>
 
 #include "cdx_common.h"
@@ -42,7 +43,7 @@ __device__ __forceinline__ float wave_sum_dpp(float v) {
 template <int VPL, bool FULL, bool HAS_RES, bool STORE_RES>
 __global__ __launch_bounds__(64 * kWavesPerBlock) void add_rmsnorm_kernel(
     const uint16_t* x, const uint16_t* res, const uint16_t* __restrict__ w, float eps,
-    int64_t T, int H, uint16_t* out, uint16_t* res_out) {
+    int64_t T, int H, uint16_t* out, int64_t ldo, uint16_t* res_out) {
   const int lane = threadIdx.x & 63;
   const int64_t nwaves = (int64_t)gridDim.x * kWavesPerBlock;
   int64_t row = (int64_t)blockIdx.x * kWavesPerBlock + (threadIdx.x >> 6);
@@ -102,7 +103,7 @@ __global__ __launch_bounds__(64 * kWavesPerBlock) void add_rmsnorm_kernel(
     }
     const float inv = rsqrtf(wave_sum_dpp(ss) / (float)H + eps);
 
-    uint4* orow = reinterpret_cast<uint4*>(out + row * H);
+    uint4* orow = reinterpret_cast<uint4*>(out + row * ldo);
     uint4* hrow = STORE_RES ? reinterpret_cast<uint4*>(res_out + row * H) : nullptr;
 #pragma unroll
     for (int v = 0; v < VPL; ++v) {
@@ -123,7 +124,7 @@ __global__ __launch_bounds__(64 * kWavesPerBlock) void add_rmsnorm_kernel(
 
 template <int VPL, bool FULL>
 int launch_vpl(const uint16_t* x, const uint16_t* res, const uint16_t* w, float eps, int64_t T,
-               int H, uint16_t* out, uint16_t* res_out, hipStream_t s) {
+               int H, uint16_t* out, int64_t ldo, uint16_t* res_out, hipStream_t s) {
   // Four blocks (16 waves) per CU; each wave walks about T / waves rows, so that its
   // prefetch of the next row has work to hide behind.
   const int64_t max_blocks = (int64_t)device_cu_count() * 4;
@@ -131,20 +132,30 @@ int launch_vpl(const uint16_t* x, const uint16_t* res, const uint16_t* w, float 
   const dim3 grid((unsigned)blocks);
   const dim3 block(64 * kWavesPerBlock);
   if (res == nullptr) {
-    add_rmsnorm_kernel<VPL, FULL, false, false><<<grid, block, 0, s>>>(x, res, w, eps, T, H, out, res_out);
+    add_rmsnorm_kernel<VPL, FULL, false, false><<<grid, block, 0, s>>>(x, res, w, eps, T, H, out, ldo, res_out);
   } else if (res_out == nullptr) {
-    add_rmsnorm_kernel<VPL, FULL, true, false><<<grid, block, 0, s>>>(x, res, w, eps, T, H, out, res_out);
+    add_rmsnorm_kernel<VPL, FULL, true, false><<<grid, block, 0, s>>>(x, res, w, eps, T, H, out, ldo, res_out);
   } else {
-    add_rmsnorm_kernel<VPL, FULL, true, true><<<grid, block, 0, s>>>(x, res, w, eps, T, H, out, res_out);
+    add_rmsnorm_kernel<VPL, FULL, true, true><<<grid, block, 0, s>>>(x, res, w, eps, T, H, out, ldo, res_out);
   }
   return check_launch("cdx_add_rmsnorm_fwd");
 }
 
 template <int VPL>
 int launch_h(const uint16_t* x, const uint16_t* res, const uint16_t* w, float eps, int64_t T, int H,
-             uint16_t* out, uint16_t* res_out, hipStream_t s) {
-  if (H == 512 * VPL) return launch_vpl<VPL, true>(x, res, w, eps, T, H, out, res_out, s);
-  return launch_vpl<VPL, false>(x, res, w, eps, T, H, out, res_out, s);
+             uint16_t* out, int64_t ldo, uint16_t* res_out, hipStream_t s) {
+  if (H == 512 * VPL) return launch_vpl<VPL, true>(x, res, w, eps, T, H, out, ldo, res_out, s);
+  return launch_vpl<VPL, false>(x, res, w, eps, T, H, out, ldo, res_out, s);
+}
+
+int launch(const uint16_t* x, const uint16_t* res, const uint16_t* w, float eps, int64_t T, int H,
+           uint16_t* out, int64_t ldo, uint16_t* res_out, hipStream_t s) {
+  const int nvec = H / 8;
+  if (nvec <= 64) return launch_h<1>(x, res, w, eps, T, H, out, ldo, res_out, s);
+  if (nvec <= 128) return launch_h<2>(x, res, w, eps, T, H, out, ldo, res_out, s);
+  if (nvec <= 256) return launch_h<4>(x, res, w, eps, T, H, out, ldo, res_out, s);
+  if (nvec <= 512) return launch_h<8>(x, res, w, eps, T, H, out, ldo, res_out, s);
+  return launch_h<16>(x, res, w, eps, T, H, out, ldo, res_out, s);
 }
 
 }  // namespace
@@ -166,11 +177,22 @@ extern "C" int cdx_add_rmsnorm_fwd(const uint16_t* x, const uint16_t* residual,
   if (!aligned16(x) || !aligned16(weight) || !aligned16(out) || (residual && !aligned16(residual)) ||
       (residual_out && !aligned16(residual_out)))
     return fail(CDX_EUNSUPPORTED, "cdx_add_rmsnorm_fwd: pointers must be 16-byte aligned");
-  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
-  const int nvec = H / 8;
-  if (nvec <= 64) return launch_h<1>(x, residual, weight, eps, T, H, out, residual_out, s);
-  if (nvec <= 128) return launch_h<2>(x, residual, weight, eps, T, H, out, residual_out, s);
-  if (nvec <= 256) return launch_h<4>(x, residual, weight, eps, T, H, out, residual_out, s);
-  if (nvec <= 512) return launch_h<8>(x, residual, weight, eps, T, H, out, residual_out, s);
-  return launch_h<16>(x, residual, weight, eps, T, H, out, residual_out, s);
+  return launch(x, residual, weight, eps, T, H, out, H, residual_out, reinterpret_cast<hipStream_t>(stream));
+}
+
+extern "C" int cdx_rmsnorm_ld_fwd(const uint16_t* x, const uint16_t* weight, float eps, int64_t T, int32_t H,
+                                  uint16_t* out, int64_t ldo, void* stream) {
+  using namespace cdx;
+  clear_error();
+  const char* name = "cdx_rmsnorm_ld_fwd";
+  if (T < 0 || H <= 0) return fail(CDX_EINVAL, "%s: bad shape T=%lld H=%d", name, (long long)T, H);
+  if (H % 8 != 0 || H > 8192) return fail(CDX_EUNSUPPORTED, "%s: H=%d must be a multiple of 8 and <= 8192", name, H);
+  if (!(eps >= 0.f)) return fail(CDX_EINVAL, "%s: eps must be >= 0", name);
+  if (ldo < H) return fail(CDX_EINVAL, "%s: ldo=%lld is smaller than H=%d", name, (long long)ldo, H);
+  if (ldo % 8 != 0) return fail(CDX_EUNSUPPORTED, "%s: ldo=%lld must be a multiple of 8", name, (long long)ldo);
+  if (T == 0) return CDX_OK;
+  if (!x || !weight || !out) return fail(CDX_EINVAL, "%s: null x/weight/out", name);
+  if (!aligned16(x) || !aligned16(weight) || !aligned16(out))
+    return fail(CDX_EUNSUPPORTED, "%s: pointers must be 16-byte aligned", name);
+  return launch(x, nullptr, weight, eps, T, H, out, ldo, nullptr, reinterpret_cast<hipStream_t>(stream));
 }

@@ -68,6 +68,19 @@ int cdx_add_rmsnorm_fwd(const uint16_t* x_dev, const uint16_t* residual_dev,
                         const uint16_t* weight_dev, float eps, int64_t T, int32_t H,
                         uint16_t* out_dev, uint16_t* residual_out_dev, void* stream);
 
+/*
+ * Plain RMSNorm (cdx_add_rmsnorm_fwd with residual == NULL) whose output rows sit at
+ * a stride ldo >= H (a multiple of 8): out[t * ldo + c] for c < H; the columns past
+ * H are not touched.  x [T, H] contiguous.  The model writes the next layer's
+ * normalised x into the left half of a [T, 2H] buffer whose right half
+ * cdx_mu_guidance_fwd fills with mu, so that the projection reads [x | mu] as one
+ * operand.
+ *
+ * Replaces: core/normalization.py:29-32 (the block's input_layernorm, core/layer.py:166).
+ */
+int cdx_rmsnorm_ld_fwd(const uint16_t* x_dev, const uint16_t* weight_dev, float eps, int64_t T, int32_t H,
+                       uint16_t* out_dev, int64_t ldo, void* stream);
+
 /* ---- piece 1a: routing plan ------------------------------------------------ */
 
 /* Bytes of workspace cdx_route_plan needs for T tokens and E experts: one int32 per
@@ -305,7 +318,8 @@ int cdx_mu_qkv_rope_bcast_fwd(const uint16_t* x_dev, int64_t ldx, const uint16_t
  * mu guidance, the producer of the next layer's mu operand:
  *   out[t, n] = clamp(sum_k h[t, k] w[n, k] + clamp(mu[n], mu_lo, mu_hi), lo, hi)
  * h [T, H] bf16, w [H, H] bf16 (nn.Linear layout, [out, in]), mu [H] bf16 (the
- * MuGuidance parameter, read on every call), out [T, H] bf16; fp32 accumulation, one
+ * MuGuidance parameter, read on every call), out [T, H] bf16 with rows at stride
+ * ldo >= H (a multiple of 8; H for a contiguous output); fp32 accumulation, one
  * rounding.  (mu_lo, mu_hi) are the module's (mu_min, mu_max); the model passes
  * (lo, hi) = (-2, 2), its clamp of mu between layers, the module API (-inf, +inf).
  * H must be a multiple of 64.
@@ -315,7 +329,7 @@ int cdx_mu_qkv_rope_bcast_fwd(const uint16_t* x_dev, int64_t ldx, const uint16_t
  */
 int cdx_mu_guidance_fwd(const uint16_t* h_dev, int64_t T, int32_t H, const uint16_t* w_dev,
                         const uint16_t* mu_dev, float mu_lo, float mu_hi, float lo, float hi,
-                        uint16_t* out_dev, void* stream);
+                        uint16_t* out_dev, int64_t ldo, void* stream);
 
 /*
  * Causal GQA attention over the fused projection's outputs:

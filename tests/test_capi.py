@@ -63,6 +63,15 @@ def test_norm_validation(lib):
     assert lib.cdx_add_rmsnorm_fwd(16, None, 16, 1e-6, 4, 8, 16, 32, None) == CDX_EINVAL  # residual_out w/o residual
     assert lib.cdx_add_rmsnorm_fwd(18, None, 16, 1e-6, 4, 8, 16, None, None) == CDX_EUNSUPPORTED  # misaligned
     assert lib.cdx_add_rmsnorm_fwd(None, None, None, 1e-6, 0, 8, None, None, None) == 0  # T == 0 is a no-op
+    # the strided-output plain norm: (x, weight, eps, T, H, out, ldo)
+    assert lib.cdx_rmsnorm_ld_fwd(16, 16, 1e-6, 4, 64, 16, 32, None) == CDX_EINVAL  # ldo < H
+    assert lib.cdx_rmsnorm_ld_fwd(16, 16, 1e-6, 4, 64, 16, 132, None) == CDX_EUNSUPPORTED  # ldo % 8
+    assert lib.cdx_rmsnorm_ld_fwd(16, 16, 1e-6, 4, 60, 16, 128, None) == CDX_EUNSUPPORTED  # H % 8
+    assert lib.cdx_rmsnorm_ld_fwd(16, 16, -1.0, 4, 64, 16, 128, None) == CDX_EINVAL  # eps
+    assert lib.cdx_rmsnorm_ld_fwd(None, 16, 1e-6, 4, 64, 16, 128, None) == CDX_EINVAL
+    assert lib.cdx_rmsnorm_ld_fwd(16, 16, 1e-6, 4, 64, 24, 128, None) == CDX_EUNSUPPORTED  # misaligned out
+    assert b"cdx_rmsnorm_ld_fwd" in lib.cdx_last_error()
+    assert lib.cdx_rmsnorm_ld_fwd(None, None, 1e-6, 0, 64, None, 128, None) == 0  # T == 0
 
 
 def test_route_validation(lib):
@@ -123,8 +132,11 @@ def test_gemm_validation(lib):
     assert b"multiple of 64" in lib.cdx_last_error()
     # gate/up operand beyond 4 GB: (64 + 1) * 2 * 8192 * 8192 * 2 bytes
     assert lib.cdx_moe_swiglu_fwd(16, 8, 8192, 8192, 64, 1, 16, 16, 16, 16, 16, 16, None) == CDX_EUNSUPPORTED
-    assert lib.cdx_mu_guidance_fwd(16, 8, 64, 16, 16, 2.0, 0.0, -2.0, 2.0, 16, None) == CDX_EINVAL  # mu_lo > mu_hi
-    assert lib.cdx_mu_guidance_fwd(16, 8, 64, 16, None, 0.0, 2.0, -2.0, 2.0, 16, None) == CDX_EINVAL  # no mu
+    assert lib.cdx_mu_guidance_fwd(16, 8, 64, 16, 16, 2.0, 0.0, -2.0, 2.0, 16, 64, None) == CDX_EINVAL  # mu_lo > mu_hi
+    assert lib.cdx_mu_guidance_fwd(16, 8, 64, 16, None, 0.0, 2.0, -2.0, 2.0, 16, 64, None) == CDX_EINVAL  # no mu
+    assert lib.cdx_mu_guidance_fwd(16, 8, 64, 16, 16, 0.0, 2.0, -2.0, 2.0, 16, 32, None) == CDX_EINVAL  # ldo < H
+    assert lib.cdx_mu_guidance_fwd(16, 8, 64, 16, 16, 0.0, 2.0, -2.0, 2.0, 16, 68, None) == CDX_EUNSUPPORTED  # ldo % 8
+    assert lib.cdx_mu_guidance_fwd(None, 0, 64, None, None, 0.0, 2.0, -2.0, 2.0, None, 128, None) == 0  # T = 0
     assert lib.cdx_linear_fwd(16, 64, 16, 64, 8, 64, 30, 16, 30, None) == CDX_EINVAL  # ldo < round_up(N, 8)
     assert lib.cdx_linear_residual_fwd(16, 64, 16, 64, 8, 64, 30, 16, 32, None) == CDX_EUNSUPPORTED  # N % 8
     assert lib.cdx_linear_residual_fwd(16, 96, 16, 96, 8, 96, 32, 16, 32, None) == CDX_EUNSUPPORTED  # K % 64

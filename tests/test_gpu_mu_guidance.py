@@ -76,3 +76,23 @@ def test_mu_guidance_follows_data_writes(cdx):
         ref = 1.5 + h.float().cpu() @ m.mu_proj.weight.float().cpu().t()
     assert not torch.equal(before, after)
     assert_close_bf16(after, ref, "after .data writes")
+
+
+@pytest.mark.parametrize("T,H", [(16384, 2048), (300, 768), (5, 64)])
+def test_mu_guidance_into_the_right_half_of_a_pair(cdx, T, H):
+    """Written into the right half of a [T, 2H] buffer (output rows at stride 2H, as the
+    model places mu beside the next layer's x): the same bits as the contiguous output,
+    and the left half untouched."""
+    from complexity_deep.layer import mu_guidance
+    print(f"mu_guidance into a pair T={T} H={H}", flush=True)
+    g = torch.Generator().manual_seed(T * 3 + H)
+    h = torch.randn(T, H, generator=g).to(bf16).cuda()
+    w = (torch.randn(H, H, generator=g) / math.sqrt(H)).to(bf16).cuda()
+    mu_param = torch.linspace(-1.0, 3.0, H).to(bf16).cuda()
+    ref = mu_guidance(h, w, mu_param, 0.0, 2.0, -2.0, 2.0)
+    pair = torch.full((T, 2 * H), 7.0, dtype=bf16, device="cuda")
+    out = mu_guidance(h, w, mu_param, 0.0, 2.0, -2.0, 2.0, out=pair[:, H:])
+    torch.cuda.synchronize()
+    assert out.data_ptr() == pair[:, H:].data_ptr()
+    assert torch.equal(pair[:, H:], ref)
+    assert bool((pair[:, :H] == 7.0).all()), "the left half was written"

@@ -54,6 +54,24 @@ def test_plain_rmsnorm_matches_oracle(cdx, oracle, T, H):
     assert_close_bf16(y.view(T, H), oracle.rms_norm(x.float(), w.float(), 1e-6), "rmsnorm")
 
 
+@pytest.mark.parametrize("T,H", [(16384, 2048), (2048, 768), (5, 1000), (3, 8)])
+def test_rmsnorm_into_the_left_half_of_a_pair(cdx, T, H):
+    """cdx_rmsnorm_ld_fwd: output rows at stride 2H (the left half of a [T, 2H] buffer, as
+    the model places the next layer's x beside its mu) hold the same bits as the
+    contiguous plain norm, and the right half is untouched."""
+    from complexity_deep.normalization import rms_norm
+    print(f"rmsnorm into a pair T={T} H={H}", flush=True)
+    x, _, w = _data(T, H, 23)
+    x, w = x.cuda(), w.cuda()
+    ref = rms_norm(x, w, 1e-6)
+    pair = torch.full((T, 2 * H), 7.0, dtype=bf16, device="cuda")
+    out = rms_norm(x.view(1, T, H), w, 1e-6, out=pair[:, :H].view(1, T, H))
+    torch.cuda.synchronize()
+    assert out.data_ptr() == pair.data_ptr()
+    assert torch.equal(pair[:, :H], ref)
+    assert bool((pair[:, H:] == 7.0).all()), "the right half was written"
+
+
 def test_empty_and_large_eps(cdx, oracle):
     from complexity_deep.normalization import add_rms_norm
     e = torch.empty(0, 64, dtype=bf16, device="cuda")

@@ -187,6 +187,7 @@ def test_cached_decode_step_keeps_the_reference_sdpa_alignment(cdx):
     (32, 520, 1024, 8, 4, "full", 3, True),        # D = 128, S % 16 != 0: waves span two sequences
     (32, 384, 1024, 8, 2, "broadcast", 5, True),   # D = 128, 48 x 6 tiles, M tiles span sequences
     (24, 512, 1024, 8, 4, "full", 0, False),       # D = 128 without QK norm, 48 x 8 tiles
+    (16, 1024, 1024, 8, 4, None, 0, True),         # D = 128 without mu: the persistent form with dense A
 ])
 def test_qkv_rope_many_tiles(cdx, oracle, B, S, H, nq, nkv, mu_mode, pos0, qk_norm):
     """More tiles than CUs at each head dim, V stored plain and transposed (the
@@ -350,3 +351,32 @@ def test_broadcast_mu_fold(cdx, oracle, B, S, H, nq, nkv, vt):
     assert_close_bf16(got[0][:1], rq, "q")
     assert_close_bf16(got[1][:1], rk, "k")
     assert_close_bf16(got[2][:1], rv, "v")
+
+
+@pytest.mark.parametrize("B,S,H,nq,nkv,vt", [
+    (8, 1024, 2048, 16, 8, True),   # 1B heads, 512 tiles: the persistent form
+    (2, 256, 768, 12, 4, False),    # README size, D = 64
+    (1, 77, 256, 4, 2, True),       # D = 64, ragged
+])
+def test_side_by_side_operands(cdx, B, S, H, nq, nkv, vt):
+    """x and mu as the two halves of one [B, S, 2H] buffer (how the model lays them out)
+    and the module's [N, 2H] weights: the projection then runs as one dense K = 2H
+    contraction, which must give the bits of the two-source form on separate tensors."""
+    from complexity_deep.attention import mu_qkv_rope
+    from complexity_deep.rotary import RotaryEmbedding
+    D = H // nq
+    N = (nq + 2 * nkv) * D
+    print(f"side-by-side operands B={B} S={S} H={H} heads={nq}/{nkv} D={D} vt={vt}", flush=True)
+    g = torch.Generator().manual_seed(B + S + H)
+    pair = torch.randn(B, S, 2 * H, generator=g).clamp(-2, 2).to(bf16).cuda()
+    w = (torch.randn(N, 2 * H, generator=g) * 0.02).to(bf16).cuda()
+    qn = (1 + 0.1 * torch.randn(D, generator=g)).to(bf16).cuda()
+    kn = (1 + 0.1 * torch.randn(D, generator=g)).to(bf16).cuda()
+    table = RotaryEmbedding(D).cuda().cos_sin_table(S, torch.device("cuda"))
+    side = mu_qkv_rope(pair[..., :H], pair[..., H:], w[:, :H], H, nq, nkv, D, qn, kn, 1e-6, table, 0,
+                       v_transposed=vt, w_mu=w[:, H:])
+    apart = mu_qkv_rope(pair[..., :H].contiguous(), pair[..., H:].contiguous(), w[:, :H].contiguous(), H, nq,
+                        nkv, D, qn, kn, 1e-6, table, 0, v_transposed=vt, w_mu=w[:, H:].contiguous())
+    torch.cuda.synchronize()
+    for a, b, what in zip(side, apart, "qkv"):
+        assert torch.equal(a, b), f"{what} differs between the dense and the two-source form"
