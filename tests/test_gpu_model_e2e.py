@@ -205,6 +205,29 @@ def test_cfg5_route_stress_forward(cdx, oracle):
             _check(seqs[j:j + 1], ref, f"cfg5 logits, sequence {b}")
 
 
+@pytest.mark.parametrize("B,S", [(4, 512), (3, 333)])
+def test_side_by_side_forward_equals_separate_operands(cdx, monkeypatch, B, S):
+    """The model's forward writes each next layer's normalised input and mu into the two
+    halves of one [B, S, 2H] buffer, so that the projection reads one operand.  With that
+    buffer switched off (x and mu as separate tensors, the two-source projection) the
+    logits must be the same bits: the re-layout changes no sum and no rounding."""
+    from complexity_deep import layer as L
+    from complexity_deep import synthetic as syn
+    print(f"side-by-side forward vs separate operands, README model {B} x {S}", flush=True)
+    cfg = readme_config(cdx)
+    m = _build(cdx, cfg, seed=3)
+    with torch.no_grad():
+        m.mu_init.normal_(0, 0.5)  # a non-zero layer-0 mu, folded in both runs
+    ids = syn.zipf_token_ids(B, S, cfg.vocab_size, seed=3).cuda()
+    with torch.no_grad():
+        side = m(ids).logits.clone()
+        orig = L.TransformerBlock.forward_fused
+        monkeypatch.setattr(L.TransformerBlock, "forward_fused",
+                            lambda self, *a, **kw: orig(self, *a, **{**kw, "pair": None}))
+        apart = m(ids).logits.clone()
+    assert torch.equal(side, apart)
+
+
 def _small(cdx):
     return cdx.ComplexityConfig(vocab_size=2048, hidden_size=256, intermediate_size=704, num_hidden_layers=3,
                                 num_attention_heads=4, num_key_value_heads=2, num_experts=4)
