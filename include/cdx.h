@@ -249,6 +249,11 @@ int cdx_swiglu_fwd(const void* gate_dev, const void* up_dev, int64_t n, int32_t 
  *                  two halves of one [N, 2H] pack (w_mu = w_x + H, ldw = 2H).
  *   out    [M, N]  leading dim ldo; q = cols [0, Nq*D), k, v follow.
  * H % 64 == 0.
+ * When x and mu are the two halves of one [M, 2H] buffer and w_x and w_mu the two
+ * halves of one [N, 2H] buffer, the same product is the call with mu == NULL, x = that
+ * buffer (ldx = 2H), w_x = the weight buffer (ldw = 2H) and 2H in place of H: one
+ * operand on each side, the same sums in the same order (bit-identical), and no
+ * choice between two sources on every load (this holds for cdx_mu_qkv_rope_fwd too).
  *
  * Replaces: core/attention.py:120-131 (cat + three F.linear),
  * cuda/triton_mu_qkv.py:195-283 (fused_mu_qkv_projection).
