@@ -6,8 +6,8 @@
   the ``inv_freq`` buffer.  Checked against float64 cos/sin of the exact angles; the
   bound (3e-4) covers the fp32 rounding of p * inv_freq at p < 2048, while angles
   from a bf16-rounded inv_freq are off by whole radians there.
-* Projection weights: q/k/v_proj and mu_to_q/k/v weights are row views of the
-  [2, N, H] buffer the kernel reads (QKVWeights), so writes through ``.data`` (the
+* Projection weights: q/k/v_proj and mu_to_q/k/v weights are views of the column
+  halves of the [N, 2H] buffer the kernel reads (QKVWeights), so writes through ``.data`` (the
   pattern of the reference's run_ablations.py:45-78) reach the kernel operand; the
   views survive load_state_dict and are re-established after a cast or move.
 """
@@ -71,6 +71,8 @@ def test_qkv_weights_are_views_of_the_kernel_operand():
     sd0 = {k: v.clone() for k, v in a.state_dict().items()}
     w_x, w_mu = a.qkv_weights()
     assert w_x.shape == (256 + 2 * 128, 256) and w_mu.shape == w_x.shape
+    # side by side: row n of one [N, 2H] buffer is [W_x[n] | W_mu[n]]
+    assert w_x.stride() == (512, 1) and w_mu.data_ptr() == w_x.data_ptr() + 256 * w_x.element_size()
     assert torch.equal(w_x, torch.cat([sd0["q_proj.weight"], sd0["k_proj.weight"], sd0["v_proj.weight"]]))
     assert torch.equal(w_mu, torch.cat([sd0["mu_to_q.weight"], sd0["mu_to_k.weight"], sd0["mu_to_v.weight"]]))
     # Binding changes neither keys nor values.
