@@ -14,7 +14,9 @@ References, on the same bf16 inputs:
   * the MoE: oracle.token_routed_mlp (fp32, pinned by a per-token brute force);
   * attention: oracle.causal_attention (fp32, pinned by SDPA);
   * the add + RMSNorm: oracle.add_rms_norm, and the bf16 add bit for bit;
-  * layer 0's folded projection (a broadcast mu row): the unfolded K = 2H contraction.
+  * layer 0's folded projection (a broadcast mu row): the unfolded K = 2H contraction;
+  * the norm and mu guidance writing into the halves of a [T, 2H] buffer: their
+    contiguous outputs, bit for bit.
 Bound: the bf16 tolerance of the north star (max rel err <= 2e-2 normwise, mean abs err
 <= 1e-3 against the fp32 reference rounded to bf16), checked by ``assert_close_bf16``.
 """
@@ -240,3 +242,29 @@ def test_random_broadcast_mu_fold(cdx, case):
         ulp = torch.where(b == 0, torch.zeros_like(b), 2.0 ** (torch.floor(torch.log2(b.abs())) - 7))
         excess = float(((a - b).abs() - ulp - 2.0 ** -14 * b.abs().max()).max())
         assert excess <= 0, f"random mu: {what} off the unfolded contraction by {excess:.3g} beyond the bound"
+
+
+@pytest.mark.parametrize("case", range(6))
+def test_random_norm_and_mu_guidance_into_a_pair(cdx, case):
+    """The model's side-by-side writers on random shapes: the plain norm into the left
+    half and mu guidance into the right half of a [T, 2H] buffer (rows at stride 2H)
+    give the bits of their contiguous outputs and leave the other half alone."""
+    from complexity_deep.layer import mu_guidance
+    from complexity_deep.normalization import rms_norm
+    rng = random.Random(8000 + case)
+    T = _log_int(rng, 1, 20000)
+    H = 64 * _log_int(rng, 1, 64)
+    print(f"pair writers case {case}: T={T} H={H}", flush=True)
+    g = torch.Generator().manual_seed(case)
+    h = torch.randn(T, H, generator=g).to(bf16).cuda()
+    nw = (1 + 0.1 * torch.randn(H, generator=g)).to(bf16).cuda()
+    w = (torch.randn(H, H, generator=g) * H ** -0.5).to(bf16).cuda()
+    mu_param = (torch.rand(H, generator=g) * 3 - 0.5).to(bf16).cuda()
+    pair = torch.full((T, 2 * H), -3.0, dtype=bf16, device="cuda")
+    rms_norm(h, nw, 1e-6, out=pair[:, :H])
+    mu_guidance(h, w, mu_param, 0.0, 2.0, -2.0, 2.0, out=pair[:, H:])
+    x_ref = rms_norm(h, nw, 1e-6)
+    mu_ref = mu_guidance(h, w, mu_param, 0.0, 2.0, -2.0, 2.0)
+    torch.cuda.synchronize()
+    assert torch.equal(pair[:, :H], x_ref), f"norm into a pair T={T} H={H}"
+    assert torch.equal(pair[:, H:], mu_ref), f"mu guidance into a pair T={T} H={H}"
