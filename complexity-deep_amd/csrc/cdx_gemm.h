@@ -454,9 +454,18 @@ __global__ __launch_bounds__(kGemmThreads, Cfg::MINB) void gemm_nt_kernel(const 
   const __amdgpu_buffer_rsrc_t rs_a =
       AL == ALoad::kSegmented ? make_rsrc((const void*)a_base, (uint32_t)((m_end - m0) * p.lda * 2))
                               : make_rsrc((const void*)a_base);
-  GuTile gu{};
-  if constexpr (kGuTiles) gu = gu_tile(p.b, p.ldb, p.gu_P, p.gu_shared != 0, e, n0);
-  const __amdgpu_buffer_rsrc_t rs_b = make_rsrc(bexp + (int64_t)n0 * p.ldb);
+  // SwiGLU tiles: this wave's B rows come from before or after the tile's block switch
+  // (gu_tile).  The switch row is a multiple of 128 and a wave's B rows one aligned run
+  // of BN / 4 (64, 32 or 16) rows, so they all lie on one side of it: one descriptor
+  // for the whole K loop.
+  const __amdgpu_buffer_rsrc_t rs_b = [&]() __attribute__((always_inline)) {
+    if constexpr (kGuTiles) {
+      const GuTile gu = gu_tile(p.b, p.ldb, p.gu_P, p.gu_shared != 0, e, n0);
+      return make_rsrc((const void*)(wave * (kBN / 4) >= gu.split ? gu.hi : gu.lo));
+    } else {
+      return make_rsrc(bexp + (int64_t)n0 * p.ldb);
+    }
+  }();
   // kSharedB: b_base serves the expert columns (column 0 = K column k_split), b2_base
   // the shared ones.
   const uintptr_t b_base =
@@ -570,12 +579,6 @@ __global__ __launch_bounds__(kGemmThreads, Cfg::MINB) void gemm_nt_kernel(const 
         buf_dma16(live ? r : rs_none, b_off[d - LD_A], (uint32_t)k0 * 2, dst + b_dma_off + (d - LD_A) * 1024);
       } else if constexpr (kSharedB) {
         const __amdgpu_buffer_rsrc_t r = make_rsrc((const void*)(k0 < p.k_split ? b2_base : b_base));
-        buf_dma16(live ? r : rs_none, b_off[d - LD_A], (uint32_t)k0 * 2, dst + b_dma_off + (d - LD_A) * 1024);
-      } else if constexpr (kGuTiles) {
-        // The instruction's rows start at wave * BN/4 + 8 j (a multiple of 8; split is a
-        // multiple of 128, so all eight rows lie on one side of it).
-        const int row0 = wave * (kBN / 4) + (d - LD_A) * ROWS_PER_DMA;
-        const __amdgpu_buffer_rsrc_t r = make_rsrc((const void*)(row0 >= gu.split ? gu.hi : gu.lo));
         buf_dma16(live ? r : rs_none, b_off[d - LD_A], (uint32_t)k0 * 2, dst + b_dma_off + (d - LD_A) * 1024);
       } else {
         buf_dma16(live ? rs_b : rs_none, b_off[d - LD_A], (uint32_t)k0 * 2, dst + b_dma_off + (d - LD_A) * 1024);

@@ -122,10 +122,12 @@ __global__ __launch_bounds__(kGemmThreads, 1) void gemm_persist_kernel(const Gem
   // scalars: a struct selected through a reference ends up in scratch memory.
   // Grouped: m0 / m_end are the tile's rows in the sorted order, its expert's B rows
   // start at b + e * b_estride, and A is the whole gather source.
-  // Gathered (SwiGLU) tiles: b and b2 are the bases of the rows before and after the
-  // tile's block switch at row `split` (gu_tile).
+  // Gathered (SwiGLU) tiles: b is the base of this wave's B rows, taken before or
+  // after the tile's block switch (gu_tile).  The switch row is a multiple of 128 and a
+  // wave's rows are one 64-aligned run of 64, so they all lie on one side of it: the
+  // choice is made once per tile, not for every DMA.
   auto tile_at = [&](int i, int64_t& m0, int64_t& m_end, int& n0, uintptr_t& a, uintptr_t& a2, uintptr_t& b,
-                     uintptr_t& b2, int& split, int s0v, int s1v, int civ) __attribute__((always_inline)) {
+                     uintptr_t& b2, int s0v, int s1v, int civ) __attribute__((always_inline)) {
     const int L = x_first + i;
     const int per_group = kGroupM * p.nt_count;
     const int group = L / per_group;
@@ -157,12 +159,10 @@ __global__ __launch_bounds__(kGemmThreads, 1) void gemm_persist_kernel(const Gem
       a = (uintptr_t)(p.a + m0 * p.lda);
     }
     b = (uintptr_t)(p.b + (int64_t)e * p.b_estride + (int64_t)n0 * p.ldb);
-    split = kBN;
     if constexpr (kGathered) {
       const GuTile g = gu_tile(p.b, p.ldb, p.gu_P, p.gu_shared != 0, e, n0);
-      b = g.lo;
-      b2 = g.hi;
-      split = g.split;
+      b = wave * (kBN / 4) >= g.split ? g.hi : g.lo;
+      b2 = b;
     } else if constexpr (AL == ALoad::kConcat) {
       a2 = (uintptr_t)(p.a2 + m0 * p.lda2) - (uintptr_t)p.k_split * 2;
       b2 = (uintptr_t)(p.b2 + (int64_t)n0 * p.ldb) - (uintptr_t)p.k_split * 2;
@@ -197,11 +197,11 @@ __global__ __launch_bounds__(kGemmThreads, 1) void gemm_persist_kernel(const Gem
   const __amdgpu_buffer_rsrc_t rs_none = make_rsrc(p.b, 0u);
   int ti = kx;  // index of the current tile in the XCD's range
   int64_t cur_m0, nxt_m0, cur_m_end, nxt_m_end;
-  int cur_n0, nxt_n0, cur_split, nxt_split;
+  int cur_n0, nxt_n0;
   uintptr_t cur_a, cur_a2, cur_b, cur_b2, nxt_a, nxt_a2, nxt_b, nxt_b2;
-  tile_at(ti, cur_m0, cur_m_end, cur_n0, cur_a, cur_a2, cur_b, cur_b2, cur_split, g_s0, g_s1, g_ci);
+  tile_at(ti, cur_m0, cur_m_end, cur_n0, cur_a, cur_a2, cur_b, cur_b2, g_s0, g_s1, g_ci);
   bool has_next = ti + x_blocks < x_count;
-  tile_at(has_next ? ti + x_blocks : ti, nxt_m0, nxt_m_end, nxt_n0, nxt_a, nxt_a2, nxt_b, nxt_b2, nxt_split, g_s0,
+  tile_at(has_next ? ti + x_blocks : ti, nxt_m0, nxt_m_end, nxt_n0, nxt_a, nxt_a2, nxt_b, nxt_b2, g_s0,
           g_s1, g_ci);
   // Gathered rows: the source row of each lane's DMA rows, through the permutation;
   // rows past the segment repeat its last row (loaded, never stored), and an entry
@@ -244,13 +244,7 @@ __global__ __launch_bounds__(kGemmThreads, 1) void gemm_persist_kernel(const Gem
       buf_dma16(st.live ? r : rs_none, off, (uint32_t)k0 * 2, dst + a_dma_off + d * 1024);
     } else {
       const uintptr_t first_src = st.next ? nxt_b : cur_b, second_src = st.next ? nxt_b2 : cur_b2;
-      bool second_b = second;
-      if constexpr (kGathered) {
-        // The instruction's eight rows lie on one side of the tile's block switch.
-        const int row0 = wave * (kBN / 4) + (d - LD_A) * ROWS_PER_DMA;
-        second_b = row0 >= (st.next ? nxt_split : cur_split);
-      }
-      const __amdgpu_buffer_rsrc_t r = make_rsrc((const void*)(second_b ? second_src : first_src));
+      const __amdgpu_buffer_rsrc_t r = make_rsrc((const void*)(second ? second_src : first_src));
       buf_dma16(st.live ? r : rs_none, b_off[d - LD_A], (uint32_t)k0 * 2, dst + b_dma_off + (d - LD_A) * 1024);
     }
   };
@@ -596,7 +590,6 @@ __global__ __launch_bounds__(kGemmThreads, 1) void gemm_persist_kernel(const Gem
     cur_a2 = nxt_a2;
     cur_b = nxt_b;
     cur_b2 = nxt_b2;
-    cur_split = nxt_split;
     has_next = ti + x_blocks < x_count;
     int t_s0 = 0, t_s1 = 0, t_ci = 0;
     if constexpr (kGathered) {
@@ -604,7 +597,7 @@ __global__ __launch_bounds__(kGemmThreads, 1) void gemm_persist_kernel(const Gem
       t_s1 = seg_tab[64 + lane];
       t_ci = seg_tab[128 + lane];
     }
-    tile_at(has_next ? ti + x_blocks : ti, nxt_m0, nxt_m_end, nxt_n0, nxt_a, nxt_a2, nxt_b, nxt_b2, nxt_split, t_s0,
+    tile_at(has_next ? ti + x_blocks : ti, nxt_m0, nxt_m_end, nxt_n0, nxt_a, nxt_a2, nxt_b, nxt_b2, t_s0,
             t_s1, t_ci);
     if constexpr (kGathered) {
 #pragma unroll
